@@ -1,0 +1,14 @@
+"""chia_proj_amd -- MI355X (gfx950) attention-variant forward library.
+
+Ten attention variants (sliding-window, local, dilated, block-diagonal,
+prefix-LM, ALiBi, Gemma-2 softcap, per-head temperature, ReLU, sigmoid) on one
+hand-written HIP forward core, reached through the C ABI in
+include/chia_attn.h.  ``OPS[name](q, k, v, **params)`` is the drop-in for the
+reference's ``launch_kernel(q, k, v)``.
+"""
+from .attention import attention, make_args, plan
+from .variants import OP_NAMES, OPS, core_kwargs
+
+__version__ = "0.1.0"
+
+__all__ = ["attention", "make_args", "plan", "OPS", "OP_NAMES", "core_kwargs", "__version__"]

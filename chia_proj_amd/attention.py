@@ -1,0 +1,163 @@
+"""Generic forward attention on the gfx950 core.
+
+``attention(q, k, v, **mask_and_score_params) -> o`` is the one entry point
+all ten variant modules call.  It validates on the host, allocates ``o`` with
+torch on q's device (the reference's ownership rule, e.g.
+kernels_gemini31propre_0018/bias_sliding_window_BEST.py:89), and launches
+``chia_attn_fwd`` on torch's current HIP stream, asynchronously, exactly like
+the reference's ``launch_kernel`` (which launches on the current stream and
+leaves synchronisation to the caller, extra_bench.py:12,19).
+"""
+from __future__ import annotations
+
+import math
+from collections import OrderedDict
+from typing import Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+
+PerHead = Union[None, torch.Tensor, Sequence[float]]
+
+SUPPORTED_HEAD_DIMS = (64, 128)
+_VEC_CACHE_MAX = 64
+_vec_cache: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+
+
+def _per_head_vector(vals: PerHead, heads: int, device: torch.device, name: str,
+                     positive: bool) -> Optional[torch.Tensor]:
+    """float32 [heads] device vector for a per-head parameter (cached for host values)."""
+    if vals is None:
+        return None
+    if isinstance(vals, torch.Tensor) and vals.device.type == "cuda":
+        t = vals
+        if t.shape != (heads,):
+            raise ValueError(f"{name} must have shape ({heads},), got {tuple(t.shape)}")
+        if t.device != device:
+            raise ValueError(f"{name} is on {t.device}, tensors are on {device}")
+        return t.to(torch.float32).contiguous()
+    host = torch.as_tensor(vals, dtype=torch.float32).reshape(-1)
+    if host.numel() != heads:
+        raise ValueError(f"{name} must have {heads} values, got {host.numel()}")
+    if not torch.isfinite(host).all():
+        raise ValueError(f"{name} must be finite")
+    if positive and not (host > 0).all():
+        raise ValueError(f"{name} must be > 0")
+    key = (name, device.index, tuple(host.tolist()))
+    cached = _vec_cache.get(key)
+    if cached is None:
+        cached = host.to(device)
+        _vec_cache[key] = cached
+        if len(_vec_cache) > _VEC_CACHE_MAX:
+            _vec_cache.popitem(last=False)
+    else:
+        _vec_cache.move_to_end(key)
+    return cached
+
+
+def _layout_ok(t: torch.Tensor) -> bool:
+    if t.stride(-1) != 1:
+        return False
+    if any(s % 8 for s in t.stride()[:3]):
+        return False
+    return t.data_ptr() % 16 == 0
+
+
+def make_args(*, batch: int, heads: int, seqlen: int, head_dim: int, norm: str = "softmax",
+              causal: bool = True, window: int = 0, dilation: int = 1, block: int = 0, prefix: int = 0,
+              scale: Optional[float] = None, softcap: float = 0.0, bias: float = 0.0,
+              post_scale: float = 1.0, alibi: bool = False, head_scale: bool = False) -> _lib.AttnArgs:
+    """Argument struct without tensors (for the host-only planning calls)."""
+    if norm not in _lib.NORMS:
+        raise ValueError(f"norm must be one of {sorted(_lib.NORMS)}, got {norm!r}")
+    a = _lib.AttnArgs()
+    a.norm = _lib.NORMS[norm]
+    a.batch, a.heads, a.seqlen, a.head_dim = batch, heads, seqlen, head_dim
+    a.causal = 1 if causal else 0
+    a.window = int(window or 0)
+    a.dilation = int(dilation or 1)
+    a.block = int(block or 0)
+    a.prefix = int(prefix or 0)
+    a.scale = float(1.0 / math.sqrt(head_dim) if scale is None else scale)
+    a.softcap = float(softcap or 0.0)
+    a.bias = float(bias)
+    a.post_scale = float(post_scale)
+    # planning ignores the per-head pointers' contents; non-null marks the feature
+    a.alibi_slopes = 16 if alibi else None
+    a.head_scale = 16 if head_scale else None
+    return a
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = "softmax",
+              causal: bool = True, window: int = 0, dilation: int = 1, block: int = 0, prefix: int = 0,
+              scale: Optional[float] = None, head_scale: PerHead = None, alibi_slopes: PerHead = None,
+              softcap: float = 0.0, bias: float = 0.0, post_scale: float = 1.0,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Forward attention o = norm(mod(q k^T) | mask) @ v for bf16 [B, H, S, D] tensors.
+
+    Mask: query i sees key j iff (j < prefix) or (band and block and dilation), with
+    band = 0 <= i-j (< window) when causal, |i-j| < window otherwise (window=0: no limit),
+    block: i//block == j//block, dilation: (i-j) % dilation == 0.
+    Score: (q.k) * scale * head_scale[h] + alibi_slopes[h] * (j - i), then
+    softcap * tanh(s / softcap) when softcap > 0.
+    norm: "softmax" | "sigmoid" (sigmoid(s + bias) * post_scale) | "relu" (relu(s) * post_scale).
+    """
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if q.dim() != 4:
+        raise ValueError(f"q must be 4-D [B, H, S, D], got shape {tuple(q.shape)}")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError(f"q, k, v must have the same shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError(f"q, k, v must be bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
+        raise ValueError(f"q, k, v must be on the same GPU device, got {q.device}, {k.device}, {v.device}")
+    B, H, S, D = q.shape
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS}, got {D}")
+    if min(B, H, S) < 1:
+        raise ValueError(f"empty tensor shape {tuple(q.shape)}")
+    if norm not in _lib.NORMS:
+        raise ValueError(f"norm must be one of {sorted(_lib.NORMS)}, got {norm!r}")
+    if window < 0 or block < 0 or prefix < 0 or dilation < 1:
+        raise ValueError("window, block, prefix must be >= 0 and dilation >= 1")
+    if dilation > 1 and prefix > 0:
+        raise ValueError("prefix cannot be combined with dilation > 1")
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    if not (sc > 0 and math.isfinite(sc)):
+        raise ValueError(f"scale must be finite and > 0, got {scale}")
+    if softcap < 0 or not math.isfinite(softcap):
+        raise ValueError(f"softcap must be finite and >= 0, got {softcap}")
+
+    q_, k_, v_ = (t if _layout_ok(t) else t.contiguous() for t in (q, k, v))
+    if out is None:
+        o = torch.empty_like(q_)
+    else:
+        if out.shape != q.shape or out.dtype != torch.bfloat16 or out.device != q.device:
+            raise ValueError("out must be a bf16 tensor of q's shape on q's device")
+        if not _layout_ok(out):
+            raise ValueError("out must have unit last stride, 16-byte alignment and strides that are multiples of 8")
+        o = out
+    hs = _per_head_vector(head_scale, H, q.device, "head_scale", positive=True)
+    sl = _per_head_vector(alibi_slopes, H, q.device, "alibi_slopes", positive=False)
+
+    a = make_args(batch=B, heads=H, seqlen=S, head_dim=D, norm=norm, causal=causal, window=window,
+                  dilation=dilation, block=block, prefix=prefix, scale=sc, softcap=softcap, bias=bias,
+                  post_scale=post_scale)
+    a.q, a.k, a.v, a.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
+    for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = t.stride(0), t.stride(1), t.stride(2)
+    a.head_scale = hs.data_ptr() if hs is not None else None
+    a.alibi_slopes = sl.data_ptr() if sl is not None else None
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.fwd(a, stream)
+    return o
+
+
+def plan(*, batch: int, heads: int, seqlen: int, head_dim: int, **mask_kw) -> dict:
+    """Host-only schedule statistics (tiles visited, exact visible pairs)."""
+    return _lib.plan(make_args(batch=batch, heads=heads, seqlen=seqlen, head_dim=head_dim, **mask_kw))

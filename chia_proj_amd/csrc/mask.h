@@ -1,0 +1,158 @@
+// mask.h -- visibility geometry shared by the host planner and the gfx950 kernel.
+//
+// Every mask of the reference's operator set (extra_bench.py:41,56-61) is, for
+// one query row, a contiguous interval of visible keys plus a key prefix that
+// every query sees:
+//
+//   visible(i, j) = (j < prefix) || (key_lo(i) <= j <= key_hi(i))
+//
+// Dilation ((i-j) % d == 0, extra_bench.py:56) is removed before that by
+// re-indexing: rows with i % d == r form an independent problem over the
+// sub-sequence i' = (i - r) / d, in which the remaining band / block / prefix
+// constraints are again an interval plus a prefix.  key_lo and key_hi are
+// non-decreasing in i', which is what makes the per-tile classification below
+// exact for EMPTY and FULL (a tile is FULL only if every pair is visible and
+// EMPTY only if none is).
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define CHIA_HD __host__ __device__ inline
+#else
+#define CHIA_HD inline
+#endif
+
+namespace chia {
+
+constexpr int32_t kInf = 1 << 29;  // band sentinel; seqlen is limited to < 2^28
+
+enum TileClass : int32_t { TILE_EMPTY = 0, TILE_FULL = 1, TILE_PARTIAL = 2 };
+
+// One residue class in sub-sequence coordinates.
+struct MaskGeom {
+  int32_t S;       // sub-sequence length
+  int32_t lo, hi;  // band: lo <= i' - j' <= hi  (+-kInf = unbounded)
+  int32_t prefix;  // keys j' < prefix are visible to every query
+  int32_t blk;     // block size in ORIGINAL positions, 0 = off
+  int32_t dil, r;  // original position = r + dil * sub position
+};
+
+CHIA_HD int32_t imax32(int32_t a, int32_t b) { return a > b ? a : b; }
+CHIA_HD int32_t imin32(int32_t a, int32_t b) { return a < b ? a : b; }
+
+CHIA_HD int32_t floor_div(int32_t a, int32_t b) {  // b > 0
+  int32_t q = a / b;
+  return (a % b != 0 && a < 0) ? q - 1 : q;
+}
+CHIA_HD int32_t ceil_div(int32_t a, int32_t b) {  // b > 0
+  int32_t q = a / b;
+  return (a % b != 0 && a > 0) ? q + 1 : q;
+}
+
+// First visible key of query i' (ignoring the prefix).
+CHIA_HD int32_t key_lo(const MaskGeom& g, int32_t i) {
+  int32_t v = (g.hi >= kInf) ? 0 : i - g.hi;
+  if (g.blk > 0) {
+    const int32_t io = g.r + g.dil * i;
+    const int32_t bs = (io / g.blk) * g.blk;  // first original position of the block
+    v = imax32(v, bs <= g.r ? 0 : ceil_div(bs - g.r, g.dil));
+  }
+  return imax32(v, 0);
+}
+
+// Last visible key of query i' (ignoring the prefix).
+CHIA_HD int32_t key_hi(const MaskGeom& g, int32_t i) {
+  int32_t v = (g.lo <= -kInf) ? g.S - 1 : i - g.lo;
+  if (g.blk > 0) {
+    const int32_t io = g.r + g.dil * i;
+    const int32_t be = (io / g.blk) * g.blk + g.blk - 1;  // last original position
+    v = imin32(v, (be - g.r) / g.dil);                     // be >= io >= r
+  }
+  return imin32(v, g.S - 1);
+}
+
+CHIA_HD bool visible(const MaskGeom& g, int32_t i, int32_t j) {
+  if (j < 0 || j >= g.S || i < 0 || i >= g.S) return false;
+  if (j < g.prefix) return true;
+  return j >= key_lo(g, i) && j <= key_hi(g, i);
+}
+
+// Classify queries [a, b] (a <= b <= S-1) against keys [c, d] (c <= S-1; d
+// may run past the end, those keys are treated as masked).
+CHIA_HD int32_t classify_tile(const MaskGeom& g, int32_t a, int32_t b, int32_t c, int32_t d) {
+  const bool tail = d > g.S - 1;
+  if (!tail && d < g.prefix) return TILE_FULL;
+  const int32_t ulo = key_lo(g, a), uhi = key_hi(g, b);  // hull of the rows' intervals
+  if (ulo > uhi || c > uhi || d < ulo) return c < g.prefix ? TILE_PARTIAL : TILE_EMPTY;
+  const int32_t ilo = key_lo(g, b), ihi = key_hi(g, a);  // common part of the intervals
+  if (!tail && c >= ilo && d <= ihi) return TILE_FULL;
+  return TILE_PARTIAL;
+}
+
+// KV tiles of width bn that queries [a, b] may touch: [0, n_pre) followed by
+// [start2, start2 + n2).
+struct TileRange {
+  int32_t n_pre, start2, n2;
+};
+
+CHIA_HD TileRange tile_range(const MaskGeom& g, int32_t a, int32_t b, int32_t bn) {
+  TileRange t;
+  t.n_pre = (g.prefix + bn - 1) / bn;
+  const int32_t ulo = key_lo(g, a), uhi = key_hi(g, b);
+  t.start2 = t.n_pre;
+  t.n2 = 0;
+  if (ulo <= uhi) {
+    const int32_t t0 = ulo / bn, t1 = uhi / bn;
+    t.start2 = imax32(t0, t.n_pre);
+    t.n2 = imax32(0, t1 - t.start2 + 1);
+  }
+  return t;
+}
+
+CHIA_HD int32_t tile_at(const TileRange& t, int32_t k) {
+  return k < t.n_pre ? k : t.start2 + (k - t.n_pre);
+}
+
+// Host-side parameters of the whole problem (original coordinates).
+struct MaskSpec {
+  int32_t S;
+  int32_t lo, hi;  // band in original units
+  int32_t blk, prefix, dil;
+};
+
+CHIA_HD MaskSpec make_mask_spec(int32_t S, int32_t causal, int32_t window, int32_t dilation,
+                                int32_t block, int32_t prefix) {
+  MaskSpec m;
+  m.S = S;
+  if (causal) {
+    m.lo = 0;
+    m.hi = window > 0 ? window - 1 : kInf;
+  } else if (window > 0) {
+    m.lo = -(window - 1);
+    m.hi = window - 1;
+  } else {
+    m.lo = -kInf;
+    m.hi = kInf;
+  }
+  m.blk = block;
+  m.prefix = prefix;
+  m.dil = dilation < 1 ? 1 : dilation;
+  return m;
+}
+
+CHIA_HD int32_t num_residues(const MaskSpec& m) { return imin32(m.dil, m.S); }
+
+CHIA_HD MaskGeom residue_geom(const MaskSpec& m, int32_t r) {
+  MaskGeom g;
+  g.dil = m.dil;
+  g.r = r;
+  g.S = r < m.S ? (m.S - r + m.dil - 1) / m.dil : 0;
+  g.lo = m.lo <= -kInf ? -kInf : ceil_div(m.lo, m.dil);
+  g.hi = m.hi >= kInf ? kInf : floor_div(m.hi, m.dil);
+  g.blk = m.blk;
+  const int32_t p = m.prefix > r ? ceil_div(m.prefix - r, m.dil) : 0;
+  g.prefix = imin32(p, g.S);
+  return g;
+}
+
+}  // namespace chia

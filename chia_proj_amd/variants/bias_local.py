@@ -1,0 +1,15 @@
+"""bias_local: Local (bidirectional) attention: key j visible iff |i-j| < window.
+
+Drop-in for ``launch_kernel(q, k, v)`` of the reference's ``bias_local_BEST.py``
+modules; semantics from extra_bench.py:57.  Extra keyword arguments default to the
+reference's constants.
+"""
+from ..attention import attention
+from ._spec import core_kwargs, heads_of
+
+OP = "bias_local"
+
+
+def launch_kernel(q, k, v, *, window: int = 256, scale=None):
+    """bf16 q, k, v [B, H, S, D] on the GPU -> new bf16 o of the same shape."""
+    return attention(q, k, v, **core_kwargs(OP, heads_of(q), window=window, scale=scale))

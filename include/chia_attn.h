@@ -1,0 +1,151 @@
+/*
+ * chia_attn.h -- C ABI of the MI355X (gfx950) attention-variant forward library.
+ *
+ * One forward-attention core serves all ten variants of the reference's
+ * operator set (sliding-window, local, dilated, block-diagonal, prefix-LM,
+ * ALiBi, Gemma-2 softcap, per-head temperature, ReLU and sigmoid attention).
+ * A variant is a combination of three independent parts of the argument
+ * struct: a mask (causal / window / dilation / block / prefix), a score
+ * modifier (scale, per-head scale, ALiBi slopes, softcap) and a normaliser
+ * (softmax, sigmoid or ReLU).
+ *
+ * Every entry point takes plain pointers and sizes.  Tensors are bf16 device
+ * buffers laid out [batch, heads, seqlen, head_dim] with arbitrary batch/head/
+ * seq strides (in elements) and a unit head_dim stride.  The library owns no
+ * device memory: the caller allocates q, k, v, o and the per-head vectors.
+ *
+ * Reference interface replaced (JoshiP-commits/CHIA_proj):
+ *   kernels_gemini31propre_0018/<op>_BEST.py::launch_kernel(q, k, v) -> o
+ *   (e.g. bias_sliding_window_BEST.py:87-108), whose semantics are the eager
+ *   closures of extra_bench.py:32-62 and sigmoid_fix.py:34-40.
+ */
+#ifndef CHIA_ATTN_H
+#define CHIA_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHIA_ATTN_ABI_VERSION 1
+
+/* Normaliser applied to the (modified, masked) scores.
+ *   SOFTMAX: p = softmax_j(s) over visible keys   (extra_bench.py:42)
+ *   SIGMOID: p = sigmoid(s + bias) * visible       (sigmoid_fix.py:37-39)
+ *   RELU:    p = relu(s) * visible                 (extra_bench.py:44)
+ * SIGMOID and RELU outputs are multiplied by post_scale. */
+enum chia_attn_norm {
+  CHIA_ATTN_NORM_SOFTMAX = 0,
+  CHIA_ATTN_NORM_SIGMOID = 1,
+  CHIA_ATTN_NORM_RELU = 2
+};
+
+/* Status codes.  0 is success; negative values are argument errors found on
+ * the host before any launch; positive values are hipError_t codes returned
+ * by the HIP runtime. */
+enum chia_attn_status {
+  CHIA_ATTN_OK = 0,
+  CHIA_ATTN_ERR_NULL = -1,          /* NULL args, tensor or required pointer */
+  CHIA_ATTN_ERR_SHAPE = -2,         /* batch/heads/seqlen < 1 or too large  */
+  CHIA_ATTN_ERR_HEAD_DIM = -3,      /* head_dim not in {64, 128}            */
+  CHIA_ATTN_ERR_MASK = -4,          /* negative window/block/prefix, dilation < 1,
+                                       or prefix > 0 with dilation > 1 */
+  CHIA_ATTN_ERR_SCALE = -5,         /* scale <= 0, non-finite, softcap < 0  */
+  CHIA_ATTN_ERR_NORM = -6,          /* unknown normaliser                   */
+  CHIA_ATTN_ERR_ALIGN = -7,         /* pointer/stride not 16-byte aligned   */
+  CHIA_ATTN_ERR_STRUCT = -8         /* struct_size does not match this ABI  */
+};
+
+typedef struct chia_attn_args {
+  uint32_t struct_size;   /* sizeof(chia_attn_args) */
+  uint32_t norm;          /* enum chia_attn_norm */
+
+  const void* q;          /* bf16 [B, H, S, D] */
+  const void* k;          /* bf16 [B, H, S, D] */
+  const void* v;          /* bf16 [B, H, S, D] */
+  void* o;                /* bf16 [B, H, S, D], written */
+
+  int64_t batch, heads, seqlen, head_dim;
+  int64_t q_stride[3];    /* batch, head, seq strides in elements */
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t o_stride[3];
+
+  /* Mask.  Query i sees key j iff
+   *   (j < prefix)  OR  (band(i,j) AND same_block(i,j) AND (i-j) % dilation == 0)
+   * band: causal && window>0 : 0 <= i-j < window     (extra_bench.py:61)
+   *       causal && window==0: 0 <= i-j              (extra_bench.py:41)
+   *       !causal && window>0: |i-j| < window        (extra_bench.py:57)
+   *       !causal && window==0: always
+   * same_block: block==0 or i/block == j/block       (extra_bench.py:58)
+   * prefix: prefix-LM keys visible to every query    (extra_bench.py:59)
+   * prefix > 0 cannot be combined with dilation > 1. */
+  int32_t causal;
+  int32_t window;
+  int32_t dilation;       /* >= 1; 1 = no dilation  (extra_bench.py:56) */
+  int32_t block;          /* >= 0 */
+  int32_t prefix;         /* >= 0 */
+
+  /* Score s_ij = (q_i . k_j) * scale * head_scale[h] + slope[h] * (j - i),
+   * then s = softcap * tanh(s / softcap) when softcap > 0. */
+  float scale;                /* > 0, reference 1/sqrt(D) (extra_bench.py:33) */
+  float softcap;              /* 0 = off (extra_bench.py:60) */
+  float bias;                 /* SIGMOID: added before the sigmoid */
+  float post_scale;           /* SIGMOID/RELU: multiplies p */
+  const float* head_scale;    /* device float[heads] or NULL (extra_bench.py:35,54) */
+  const float* alibi_slopes;  /* device float[heads] or NULL (extra_bench.py:36,47-50) */
+
+  int32_t reserved[8];        /* must be zero */
+} chia_attn_args;
+
+/* Launch one forward attention on `stream` (a hipStream_t; NULL = default
+ * stream).  Asynchronous: returns after the launch is queued.  Replaces
+ * launch_kernel(q, k, v) of kernels_gemini31propre_0018/<op>_BEST.py
+ * (e.g. bias_sliding_window_BEST.py:87-108). */
+int chia_attn_fwd(const chia_attn_args* args, void* stream);
+
+/* Host-only schedule statistics for `args` (no GPU call).  Used by the
+ * benchmark's FLOP accounting; the reference has no counterpart (its timer,
+ * extra_bench.py:8-22, counts latency only). */
+typedef struct chia_attn_plan_info {
+  int32_t block_m;          /* queries per workgroup */
+  int32_t block_n;          /* keys per KV tile */
+  int32_t wave_m;           /* queries per wavefront */
+  int32_t waves;            /* wavefronts per workgroup */
+  int64_t workgroups;       /* grid size */
+  int64_t tiles_total;      /* (query block, KV tile) pairs of the dense grid */
+  int64_t tiles_visited;    /* pairs the workgroups load (block_m x block_n) */
+  int64_t wave_tiles_visited; /* (wave rows, KV tile) pairs computed (wave_m x block_n) */
+  int64_t wave_tiles_partial; /* of which need the per-element mask */
+  int64_t pairs_visible;    /* exact number of visible (i, j) pairs over B*H */
+  int32_t residues;         /* dilation classes the problem splits into */
+  int32_t reserved[7];
+} chia_attn_plan_info;
+
+int chia_attn_plan(const chia_attn_args* args, chia_attn_plan_info* out);
+
+/* Host-only tile map for one residue class: out[qb * n_kt + kt] is
+ * 0 = empty, 1 = full, 2 = partial for query block qb (rows_per_block rows)
+ * and key tile kt (block_n keys), classified with the same functions the
+ * kernel uses.  n_qb/n_kt are returned through the pointers; out may be NULL
+ * to query the sizes.  out_len is the capacity of out. */
+int chia_attn_tile_map(const chia_attn_args* args, int32_t residue,
+                       int32_t rows_per_block, int32_t* n_qb, int32_t* n_kt,
+                       int8_t* out, int64_t out_len);
+
+/* Per-query visible key interval for one residue class (host-only, for tests):
+ * writes jlo[i'], jhi[i'] (sub-sequence coordinates) and the prefix length.
+ * len must be >= the residue's sub-sequence length. */
+int chia_attn_query_intervals(const chia_attn_args* args, int32_t residue,
+                              int32_t* jlo, int32_t* jhi, int32_t* prefix_len,
+                              int64_t len);
+
+const char* chia_attn_status_string(int status);
+int chia_attn_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHIA_ATTN_H */

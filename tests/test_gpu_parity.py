@@ -1,0 +1,203 @@
+"""GPU parity: the HIP core (through the C ABI) against the CPU oracle.
+
+Gate: bf16 output vs the fp32 oracle within max-abs 2e-2 and mean-abs 2e-3
+(GATE_MAX_ABS / GATE_MEAN_ABS in chia_proj_amd.gate), plus the reference's
+own gate (synth10.py:173-184: rel < 3e-2 at input scales 1.0 and 0.01).
+Full-size cases run the kernel over the whole shape and check sampled
+(batch, head) slices against the oracle.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle
+from chia_proj_amd import OPS, attention, gate
+from chia_proj_amd.workloads import baseline_configs, draw_inputs, suite
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _sample_heads(B, H, n=3):
+    picks = [(0, 0), (B - 1, H - 1), (B // 2, H // 2)]
+    out = []
+    for p in picks:
+        if p not in out:
+            out.append(p)
+    return out[:n]
+
+
+def _unnormalised(op, params):
+    """sigmoid / ReLU without the BASELINE's -log S or 1/S factor: output grows like sqrt(S)."""
+    if op == "sigmoid_attn":
+        return params.get("bias", 0.0) > -1.0
+    if op == "relu_attn":
+        return params.get("post_scale", 1.0) > 0.1
+    return False
+
+
+def _check_case(op, q, k, v, params, heads=None):
+    o = OPS[op](q, k, v, **params)
+    torch.cuda.synchronize()
+    assert o.shape == q.shape and o.dtype == torch.bfloat16
+    B, H = q.shape[:2]
+    heads = heads or _sample_heads(B, H)
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    refs = oracle.variant_ref_heads(op, qc, kc, vc, heads, **params)
+    oc = o.float().cpu()
+    for (b, h), r in zip(heads, refs):
+        res = gate.north_star_gate(r, oc[b, h], scale_aware=_unnormalised(op, params))
+        assert res.ok, f"{op} b={b} h={h}: {res.status} {res.stats}"
+
+
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("D", [64, 128])
+def test_reference_defaults_small(op, D):
+    """Every variant with the reference's constants at B1 H4 S1024."""
+    _say(f"[parity] defaults op={op} D={D}")
+    g = torch.Generator("cpu").manual_seed(1000 + D)
+    q, k, v = (torch.randn(1, 4, 1024, D, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
+    _check_case(op, q, k, v, {}, heads=[(0, h) for h in range(4)])
+
+
+@pytest.mark.parametrize("case", baseline_configs(), ids=lambda c: c.name)
+def test_baseline_configs(case):
+    """The five BASELINE.json configurations at full size (sampled heads)."""
+    _say(f"[parity] config {case.name}")
+    q, k, v, params = draw_inputs(case, DEV)
+    _check_case(case.op, q, k, v, params)
+
+
+@pytest.mark.parametrize("S", [1024, 2048, 4096])
+def test_north_star_sweep(S):
+    """All ten variants, BASELINE parameters, B4 H16 D64, S in {1024, 2048, 4096}."""
+    for case in suite(4, 16, S, 64):
+        _say(f"[parity] sweep {case.name} S={S}")
+        q, k, v, params = draw_inputs(case, DEV)
+        _check_case(case.op, q, k, v, params, heads=[(0, 0), (3, 15)])
+
+
+@pytest.mark.parametrize("op", list(OPS))
+def test_reference_gate_scales(op):
+    """The reference's verify() at input scales 1.0 and 0.01 (synth10.py:173-184)."""
+    _say(f"[parity] reference gate op={op}")
+    g = torch.Generator("cpu").manual_seed(77)
+    q, k, v = (torch.randn(1, 2, 512, 128, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
+    ok, worst, msg = gate.verify(lambda a, b, c: OPS[op](a, b, c).float().cpu(),
+                                 lambda a, b, c: oracle.variant_ref(op, a.cpu(), b.cpu(), c.cpu()), q, k, v)
+    assert ok, f"{op}: {msg}"
+
+
+EDGE = [
+    # (name, S, D, generic kwargs)
+    ("S1_causal", 1, 64, dict(causal=True)),
+    ("S7_full", 7, 64, dict(causal=False)),
+    ("S65_causal", 65, 128, dict(causal=True)),
+    ("S100_window17", 100, 64, dict(causal=True, window=17)),
+    ("S257_local40", 257, 64, dict(causal=False, window=40)),
+    ("S1000_dil3", 1000, 64, dict(causal=True, dilation=3)),
+    ("S999_dil5_w300", 999, 128, dict(causal=True, dilation=5, window=300)),
+    ("S777_block100", 777, 64, dict(causal=True, block=100)),
+    ("S777_block100_full", 777, 64, dict(causal=False, block=100)),
+    ("S600_prefix130", 600, 64, dict(causal=True, prefix=130)),
+    ("S300_prefix_ge_S", 300, 64, dict(causal=True, prefix=1000)),
+    ("S300_window_ge_S", 300, 64, dict(causal=True, window=5000)),
+    ("S300_block_ge_S", 300, 64, dict(causal=True, block=4096)),
+    ("S513_dil2_block64", 513, 64, dict(causal=True, dilation=2, block=64)),
+    ("S640_sigmoid_win", 640, 64, dict(norm="sigmoid", causal=True, window=100, bias=-1.5)),
+    ("S640_relu_local", 640, 128, dict(norm="relu", causal=False, window=70, post_scale=0.01)),
+    ("S512_softcap_window", 512, 64, dict(causal=True, window=128, softcap=20.0)),
+    ("S512_alibi_dil", 512, 64, dict(causal=True, dilation=2, alibi_slopes=[0.5, 0.25])),
+    ("S512_sigmoid_softcap_alibi", 512, 128, dict(norm="sigmoid", causal=False, softcap=10.0,
+                                                   alibi_slopes=[0.01, 0.02], bias=0.3)),
+    ("S384_relu_softcap", 384, 64, dict(norm="relu", causal=True, softcap=5.0, post_scale=0.1)),
+    ("S384_headscale", 384, 64, dict(causal=True, head_scale=[0.5, 2.0])),
+    ("S384_noncausal_block_band", 384, 64, dict(causal=False, block=32, window=3)),
+]
+
+
+@pytest.mark.parametrize("name,S,D,kw", EDGE, ids=[e[0] for e in EDGE])
+def test_edge_cases(name, S, D, kw):
+    """Ragged lengths, combined masks and modifiers through the generic entry point."""
+    _say(f"[parity] edge {name}")
+    g = torch.Generator("cpu").manual_seed(S * 7 + D)
+    q, k, v = (torch.randn(1, 2, S, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    o = attention(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+    torch.cuda.synchronize()
+    r = oracle.attention_ref(q, k, v, **kw)
+    res = gate.north_star_gate(r, o.float().cpu(), scale_aware=kw.get("norm", "softmax") != "softmax")
+    assert res.ok, f"{name}: {res.status} {res.stats}"
+
+
+def test_strided_layout_and_out_param():
+    """[B, S, H, D] storage viewed as [B, H, S, D] (non-contiguous) and a caller-provided out."""
+    _say("[parity] strided layout")
+    g = torch.Generator("cpu").manual_seed(5)
+    base = [torch.randn(2, 700, 3, 64, generator=g).to(torch.bfloat16) for _ in range(3)]
+    q, k, v = (t.to(DEV).transpose(1, 2) for t in base)  # strides (S*H*D, D, H*D, 1)
+    out = torch.empty(2, 700, 3, 64, dtype=torch.bfloat16, device=DEV).transpose(1, 2)
+    o = attention(q, k, v, causal=True, window=200, out=out)
+    assert o.data_ptr() == out.data_ptr()
+    torch.cuda.synchronize()
+    r = oracle.attention_ref(q.cpu(), k.cpu(), v.cpu(), causal=True, window=200)
+    res = gate.north_star_gate(r, o.float().cpu())
+    assert res.ok, res.stats
+
+
+def test_closed_form_row0_and_constant_v():
+    """Causal row 0 sees only key 0 (o[0] = v[0]); constant V gives constant O for softmax."""
+    _say("[parity] closed forms")
+    g = torch.Generator("cpu").manual_seed(9)
+    q, k, v = (torch.randn(1, 2, 333, 64, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
+    o = attention(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o[:, :, 0], v[:, :, 0])
+    vc = torch.full_like(v, 0.75)
+    o2 = attention(q, k, vc, causal=False, window=50)
+    torch.cuda.synchronize()
+    assert (o2.float() - 0.75).abs().max().item() < 4e-3
+
+
+def test_launch_on_current_stream():
+    """The launch is queued on torch's current stream (the reference's behaviour)."""
+    _say("[parity] stream")
+    g = torch.Generator("cpu").manual_seed(11)
+    q, k, v = (torch.randn(1, 2, 512, 64, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        o = OPS["bias_sliding_window"](q, k, v)
+    s.synchronize()
+    r = oracle.variant_ref("bias_sliding_window", q.cpu(), k.cpu(), v.cpu())
+    res = gate.north_star_gate(r, o.float().cpu())
+    assert res.ok, res.stats
+
+
+def test_deterministic():
+    """Two calls give bit-identical outputs (no atomics, fixed reduction order)."""
+    g = torch.Generator("cpu").manual_seed(12)
+    q, k, v = (torch.randn(2, 4, 1024, 64, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
+    a = OPS["bias_prefix_lm"](q, k, v)
+    b = OPS["bias_prefix_lm"](q, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_errors_raise_not_abort():
+    """Bad inputs raise Python exceptions (reference error behaviour: exceptions, shape_gen.py:97-110)."""
+    x = torch.randn(1, 2, 64, 96, device=DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        OPS["bias_local"](x, x, x)
+    y = torch.randn(1, 2, 64, 64, device=DEV)
+    with pytest.raises(TypeError):
+        OPS["bias_local"](y, y, y)
+    z = torch.randn(1, 2, 64, 64, device=DEV).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        attention(z, z, z, dilation=0)
+    with pytest.raises(ValueError):
+        OPS["temp_perhead"](z, z, z, temperature=[1.0, -1.0])
