@@ -1,0 +1,274 @@
+#!/usr/bin/env python
+"""Benchmark: the ten attention variants at B4 H16 S2048 D64 bf16 on one MI355X.
+
+One step = one call of each of the ten variants (BASELINE.json parameters) on
+inputs already resident in HBM.  Prints ONE JSON line on stdout:
+  value        whole-step algorithmic TFLOP/s (sum of the ten variants' FLOPs / step time)
+  variants     per variant: us/call (median of 3 event loops, extra_bench.py:8-22),
+               cold-cache us/call, TFLOP/s (algorithmic, visited-tile, dense),
+               fraction of the bf16 MFMA peak and of the HBM roofline
+  roofline     the dominant (slowest) variant's kernel, timed with HIP events
+               around each of its launches inside the timed steps
+  cpu_baseline the reference's eager path (restated in oracle/) on the host CPU,
+               on a bounded sample, with the GPU output checked on that sample
+Everything else goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "us/call + TFLOP/s (% bf16 MFMA peak) per variant, B4 H16 S2048 D64 bf16"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_name(op: str, D: int, params: dict) -> str:
+    from chia_proj_amd.accounting import core_plan_kwargs
+
+    kw = core_plan_kwargs(op, 16, params)
+    norm = {"softmax": 0, "sigmoid": 1, "relu": 2}[kw.get("norm", "softmax")]
+    qb = 2 if D == 64 else 1
+    al = "true" if kw["alibi"] else "false"
+    sc = "true" if kw.get("softcap", 0) else "false"
+    return f"void chia::attn_fwd_kernel<{D}, {qb}, {norm}, {al}, {sc}>(chia::FwdParams)"
+
+
+def load_traffic(kname: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/traffic.json), if recorded."""
+    path = REPO / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    return data.get(kname)
+
+
+def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16):
+    """The reference's eager bf16 path (oracle.eager_bf16, extra_bench.py:37-50) on the
+    host CPU for the first `sample_heads` head(s) of batch 0 of every variant, scaled
+    to the full step; the same sample checks the GPU output against the fp32 oracle."""
+    import torch
+
+    import oracle  # the checker and the timed CPU path; used only in this leg
+    from chia_proj_amd import gate
+    from chia_proj_amd.accounting import work
+
+    torch.set_num_threads(max(1, torch.get_num_threads()))
+    threads = torch.get_num_threads()
+    total_s = 0.0
+    total_flops = 0.0
+    checks = {}
+    for case in cases:
+        q, k, v, params = inputs[case.name]
+        B, H, S, D = case.shape
+        qs, ks, vs = (t[:1, :sample_heads].cpu() for t in (q, k, v))
+        p_sample = oracle.resolve_head_params(case.op, H, params, 0, sample_heads)
+        oracle.eager_bf16(case.op, qs, ks, vs, **p_sample)  # warm-up
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter_ns()
+            ref_eager = oracle.eager_bf16(case.op, qs, ks, vs, **p_sample)
+            ts.append((time.perf_counter_ns() - t0) * 1e-9)
+        t_sample = statistics.median(ts)
+        scale = (B * H) / sample_heads
+        total_s += t_sample * scale
+        total_flops += work(case.op, B, H, S, D, params)["flops_alg"]
+        ref32 = oracle.variant_ref(case.op, qs, ks, vs, **p_sample)
+        got = outputs[case.name][:1, :sample_heads].float().cpu()
+        unnorm = (case.op == "sigmoid_attn" and params.get("bias", 0.0) > -1.0) or (
+            case.op == "relu_attn" and params.get("post_scale", 1.0) > 0.1)
+        g = gate.north_star_gate(ref32, got, scale_aware=unnorm)
+        checks[case.op] = {"ok": g.ok, "max_abs": round(g.stats.get("max_abs", float("nan")), 6),
+                           "mean_abs": round(g.stats.get("mean_abs", float("nan")), 7),
+                           "rel_vs_eager_bf16": round(gate.relerr(ref_eager.float(), got), 6)}
+        log(f"  cpu {case.op:22s} sample {t_sample*1e3:8.1f} ms  gate {g.status} {g.stats}")
+    return {
+        "value": total_flops / total_s / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"each variant's reference bf16 eager path (oracle.eager_bf16, extra_bench.py:37-50) on "
+                   f"{sample_heads} of the {cases[0].B * cases[0].H} (batch, head) slices, median of 3 after 1 "
+                   f"warm-up, scaled by B*H/{sample_heads} to the full step; torch CPU threads={threads}"),
+        "step_s_scaled": total_s,
+        "gate_on_sample": checks,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--suite", default="headline", choices=["headline", "northstar"])
+    ap.add_argument("--variants", default="", help="comma-separated subset of variants (profiling runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cold", action="store_true")
+    ap.add_argument("--no-calibration", action="store_true")
+    ap.add_argument("--report", default="", help="also write the JSON line to this file")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the attention kernels shard over "
+                                   "(batch, head) with no exchange, so --gpus N > 1 is not provided"}))
+        return 2
+
+    import torch
+
+    from chia_proj_amd import OPS
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, PEAK_HBM_GBPS, rates, work
+    from chia_proj_amd.timing import CacheFlusher, cold_us, copy_calibration, median_us
+    from chia_proj_amd.workloads import draw_inputs, headline_suite, north_star_suite
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    cases = headline_suite() if args.suite == "headline" else north_star_suite()
+    if args.variants:
+        keep = set(args.variants.split(","))
+        cases = [c for c in cases if c.op in keep]
+        if not cases:
+            raise SystemExit(f"no variant matches {args.variants}")
+
+    log(f"[bench] device {torch.cuda.get_device_name(0)}  suite={args.suite}  variants={len(cases)}")
+    inputs, calls, works = {}, {}, {}
+    for c in cases:
+        q, k, v, params = draw_inputs(c, dev)
+        inputs[c.name] = (q, k, v, params)
+        calls[c.name] = (lambda fn=OPS[c.op], q=q, k=k, v=v, p=params: fn(q, k, v, **p))
+        works[c.name] = work(c.op, c.B, c.H, c.S, c.D, params)
+    outputs = {c.name: calls[c.name]() for c in cases}
+    torch.cuda.synchronize()
+
+    # ---- timed steps: W warm-up, then K steps bracketed by synchronize ----------
+    for _ in range(args.warmup):
+        for c in cases:
+            calls[c.name]()
+    torch.cuda.synchronize()
+    ev = {c.name: [] for c in cases}
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        for c in cases:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            calls[c.name]()
+            e1.record()
+            ev[c.name].append((e0, e1))
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_ms = start.elapsed_time(end) / args.steps
+    launch_us = {n: statistics.mean(a.elapsed_time(b) for a, b in pairs) * 1000.0 for n, pairs in ev.items()}
+    log(f"[bench] {args.steps} steps: {step_ms:.3f} ms/step (event), wall {wall*1e3/args.steps:.3f} ms/step")
+
+    # ---- per-variant: median of 3 event loops (reference timer), cold cache ----
+    flusher = None if args.no_cold else CacheFlusher(device=dev)
+    variants = {}
+    for c in cases:
+        us = median_us(calls[c.name])
+        r = rates(works[c.name], us)
+        row = {
+            "us": round(us, 2),
+            "launch_us_in_steps": round(launch_us[c.name], 2),
+            "tflops_alg": round(r["tflops_alg"], 2),
+            "tflops_visited": round(r["tflops_visited"], 2),
+            "tflops_dense": round(r["tflops_dense"], 2),
+            "pct_mfma_peak_alg": round(100 * r["frac_mfma_alg"], 2),
+            "pct_mfma_peak_visited": round(100 * r["frac_mfma_visited"], 2),
+            "pct_hbm_roofline": round(100 * r["frac_hbm"], 2),
+            "pct_roofline": round(100 * r["frac_roofline"], 2),
+            "bound": works[c.name]["bound"],
+            "visible_pct": round(100 * works[c.name]["visible_frac"], 2),
+            "tile_wave": works[c.name]["tile_wave"],
+        }
+        if flusher is not None:
+            cu = cold_us(calls[c.name], reps=15, flusher=flusher)
+            row["cold_us"] = round(cu, 2)
+            row["cold_tflops_alg"] = round(works[c.name]["flops_alg"] / (cu * 1e-6) / 1e12, 2)
+        variants[c.op] = row
+        log(f"  {c.op:22s} {us:9.1f} us  alg {r['tflops_alg']:7.1f} TF/s ({100*r['frac_mfma_alg']:5.1f}% peak)  "
+            f"visited {r['tflops_visited']:7.1f}  roofline {100*r['frac_roofline']:5.1f}%  "
+            + (f"cold {row['cold_us']:.1f} us" if "cold_us" in row else ""))
+    del flusher
+
+    # ---- dominant kernel roofline (HIP events inside the timed steps) ----------
+    dom = max(cases, key=lambda c: launch_us[c.name])
+    w = works[dom.name]
+    avg = launch_us[dom.name]
+    kname = kernel_name(dom.op, dom.D, inputs[dom.name][3])
+    if w["bound"] == "mfma":
+        achieved, peak, unit, per_launch = w["flops_alg"] / (avg * 1e-6) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", w["flops_alg"]
+    else:
+        achieved, peak, unit, per_launch = w["bytes"] / (avg * 1e-6) / 1e9, PEAK_HBM_GBPS, "GB/s", w["bytes"]
+    roofline = {
+        "bound": w["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+        "frac": round(achieved / peak, 4), "traffic": load_traffic(kname),
+        "kernel": kname, "variant": dom.op, "avg_launch_us": round(avg, 2),
+        "algorithmic_per_launch": per_launch,
+    }
+
+    calib = None if args.no_calibration else copy_calibration(device=dev)
+    if calib:
+        log(f"[bench] copy calibration: {calib['GBps']:.0f} GB/s = {100*calib['frac_of_peak']:.1f}% of 8 TB/s")
+        if calib["frac_of_peak"] >= 1.0:
+            log("[bench] WARNING: copy exceeded 100% of peak: timer not trustworthy")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline (reference eager path on the host)")
+        cpu = cpu_baseline(cases, inputs, outputs)
+
+    total_flops = sum(works[c.name]["flops_alg"] for c in cases)
+    c0 = cases[0]
+    line = {
+        "metric": METRIC,
+        "value": round(total_flops / (step_ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, BASELINE.json variant parameters)",
+        "config": {
+            "workload": (f"ten attention variants, one call each per step, B{c0.B} H{c0.H} S{c0.S} D{c0.D} bf16"
+                         + (f" (subset: {args.variants})" if args.variants else "")),
+            "batch": c0.B, "heads": c0.H, "seq_len": c0.S, "head_dim": c0.D, "suite": args.suite,
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "variants": variants,
+        "copy_calibration": calib,
+        "peak": {"bf16_mfma_tflops": PEAK_BF16_TFLOPS, "hbm_gbps": PEAK_HBM_GBPS},
+    }
+    text = json.dumps(line)
+    print(text, flush=True)
+    if args.report:
+        Path(args.report).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.report).write_text(text + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
