@@ -16,8 +16,8 @@
 namespace chia {
 
 using KernelFn = void (*)(FwdParams);
-KernelFn select_kernel_d64(int norm, bool alibi, bool softcap);
-KernelFn select_kernel_d128(int norm, bool alibi, bool softcap);
+KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
+KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap);
 
 namespace {
 
@@ -56,11 +56,40 @@ MaskSpec spec_of(const chia_attn_args* a) {
   return make_mask_spec((int32_t)a->seqlen, a->causal ? 1 : 0, a->window, a->dilation, a->block, a->prefix);
 }
 
-int block_m_of(int64_t head_dim) {
-  return kWaves * 32 * (head_dim == 64 ? TileCfg<64>::QB : TileCfg<128>::QB);
-}
+constexpr int kCUs = 256;  // MI355X compute units
 
-int wave_m_of(int64_t head_dim) { return 32 * (head_dim == 64 ? TileCfg<64>::QB : TileCfg<128>::QB); }
+// Plain causal bands (no window, no block) make a row block's work grow with
+// its position; such problems pair blocks (i, n-1-i) so every workgroup does
+// the same work.
+bool zigzag_of(const MaskSpec& m) { return m.lo >= 0 && m.hi >= kInf && m.blk == 0; }
+
+// Launch geometry shared by chia_attn_fwd and the planner.
+struct Geometry {
+  int waves;       // wavefronts per workgroup
+  int rows;        // rows per row block (32 per wavefront)
+  int n_pairs;     // row-block pairs per (b, h, residue 0)
+  int residues;
+  int zigzag;
+  int64_t workgroups;
+};
+
+Geometry geometry_of(const MaskSpec& m, int64_t batch, int64_t heads) {
+  Geometry geo;
+  geo.residues = num_residues(m);
+  geo.zigzag = zigzag_of(m) ? 1 : 0;
+  const int32_t s0 = residue_geom(m, 0).S;  // longest residue class
+  // 4 wavefronts share each K/V tile among more rows; fall back to 2 when
+  // that leaves fewer than two workgroups per CU.
+  for (int waves : {4, 2}) {
+    geo.waves = waves;
+    geo.rows = 32 * waves;
+    const int64_t nblk = (s0 + geo.rows - 1) / geo.rows;
+    geo.n_pairs = (int)((nblk + 1) / 2);
+    geo.workgroups = batch * heads * geo.residues * geo.n_pairs;
+    if (geo.workgroups >= 2 * kCUs) break;
+  }
+  return geo;
+}
 
 }  // namespace
 }  // namespace chia
@@ -105,13 +134,13 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
   p.mask = spec_of(a);
   p.B = (int32_t)a->batch;
   p.H = (int32_t)a->heads;
-  p.residues = num_residues(p.mask);
-  const int bm = block_m_of(a->head_dim);
-  const int32_t s0 = residue_geom(p.mask, 0).S;  // longest residue class
-  p.n_qblk = (s0 + bm - 1) / bm;
-  const int64_t n_wg = (int64_t)p.B * p.H * p.residues * p.n_qblk;
-  if (n_wg >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
-  p.n_wg = (int32_t)n_wg;
+  const Geometry geo = geometry_of(p.mask, a->batch, a->heads);
+  p.residues = geo.residues;
+  p.n_pairs = geo.n_pairs;
+  p.zigzag = geo.zigzag;
+  const int waves = geo.waves;
+  if (geo.workgroups >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
+  p.n_wg = (int32_t)geo.workgroups;
   p.scale = a->scale;
   p.softcap = a->softcap;
   p.bias = a->bias;
@@ -119,10 +148,10 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
 
   const bool alibi = a->alibi_slopes != nullptr;
   const bool softcap = a->softcap > 0.f;
-  KernelFn fn = a->head_dim == 64 ? select_kernel_d64((int)a->norm, alibi, softcap)
-                                  : select_kernel_d128((int)a->norm, alibi, softcap);
+  KernelFn fn = a->head_dim == 64 ? select_kernel_d64(waves, (int)a->norm, alibi, softcap)
+                                  : select_kernel_d128(waves, (int)a->norm, alibi, softcap);
   void* kargs[] = {&p};
-  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(kThreads), kargs,
+  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(64 * waves), kargs,
                                    0, (hipStream_t)stream);
   if (err != hipSuccess) return (int)err;
   err = hipGetLastError();
@@ -135,35 +164,50 @@ extern "C" int chia_attn_plan(const chia_attn_args* a, chia_attn_plan_info* out)
   if (!out) return CHIA_ATTN_ERR_NULL;
   std::memset(out, 0, sizeof(*out));
   const MaskSpec spec = spec_of(a);
-  const int bm = block_m_of(a->head_dim), wm = wave_m_of(a->head_dim);
+  const Geometry geo = geometry_of(spec, a->batch, a->heads);
   const int bn = kBN;
-  const int nres = num_residues(spec);
-  const int32_t s0 = residue_geom(spec, 0).S;
-  const int64_t n_qblk = (s0 + bm - 1) / bm;
   const int64_t bhn = a->batch * a->heads;
-  out->block_m = bm;
+  out->block_m = 2 * geo.rows;  // rows per workgroup (two row blocks)
   out->block_n = bn;
-  out->wave_m = wm;
-  out->waves = kWaves;
-  out->residues = nres;
-  out->workgroups = bhn * nres * n_qblk;
+  out->wave_m = 32;             // visited-tile unit: 32 rows x block_n keys
+  out->waves = geo.waves;
+  out->residues = geo.residues;
+  out->workgroups = geo.workgroups;
   int64_t tiles_total = 0, tiles_visited = 0, wave_tiles = 0, wave_partial = 0, pairs = 0;
-  for (int r = 0; r < nres; ++r) {
+  for (int r = 0; r < geo.residues; ++r) {
     const MaskGeom g = residue_geom(spec, r);
     if (g.S <= 0) continue;
     const int64_t nkt = (g.S + bn - 1) / bn;
-    for (int32_t q0 = 0; q0 < g.S; q0 += bm) {
-      const int32_t q1 = imin32(q0 + bm - 1, g.S - 1);
-      tiles_total += nkt;
-      const TileRange tr = tile_range(g, q0, q1, bn);
+    const int nblk = (g.S + geo.rows - 1) / geo.rows;
+    tiles_total += (int64_t)((nblk + 1) / 2) * nkt;
+    for (int pr = 0; pr < geo.n_pairs; ++pr) {
+      int b0, b1;
+      if (geo.zigzag) {
+        b0 = pr;
+        b1 = nblk - 1 - pr;
+        if (b1 < b0) continue;
+        if (b1 == b0) b1 = -1;
+      } else {
+        b0 = 2 * pr;
+        b1 = 2 * pr + 1;
+        if (b0 >= nblk) continue;
+        if (b1 >= nblk) b1 = -1;
+      }
+      const int32_t hull_hi = imin32((b1 >= 0 ? b1 : b0) * geo.rows + geo.rows - 1, g.S - 1);
+      const TileRange tr = tile_range(g, b0 * geo.rows, hull_hi, bn);
       const int n = tr.n_pre + tr.n2;
       tiles_visited += n;
       for (int it = 0; it < n; ++it) {
         const int32_t jt0 = tile_at(tr, it) * bn;
-        for (int32_t w0 = q0; w0 <= q1; w0 += wm) {
-          const int cls = classify_tile(g, w0, imin32(w0 + wm - 1, g.S - 1), jt0, jt0 + bn - 1);
-          if (cls != TILE_EMPTY) ++wave_tiles;
-          if (cls == TILE_PARTIAL) ++wave_partial;
+        for (int blk : {b0, b1}) {
+          if (blk < 0) continue;
+          for (int w = 0; w < geo.waves; ++w) {
+            const int32_t r0 = blk * geo.rows + 32 * w;
+            if (r0 >= g.S) continue;
+            const int cls = classify_tile(g, r0, imin32(r0 + 31, g.S - 1), jt0, jt0 + bn - 1);
+            if (cls != TILE_EMPTY) ++wave_tiles;
+            if (cls == TILE_PARTIAL) ++wave_partial;
+          }
         }
       }
     }

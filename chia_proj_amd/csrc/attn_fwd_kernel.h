@@ -7,13 +7,20 @@
 // Triton kernels.
 //
 // Work decomposition
-//   * one workgroup = 4 wavefronts = BM query rows of one (batch, head,
-//     dilation residue); each wavefront owns QW = 32*QB query rows;
+//   * one workgroup = NW wavefronts and a PAIR of row blocks (32 NW rows each)
+//     of one (batch, head, dilation residue); each wavefront owns 32 rows of
+//     each block (its two "query blocks" qb = 0, 1).  For causal masks without
+//     a window the pair is (i, n-1-i): every workgroup then does the same
+//     amount of work whatever the dispatcher's placement, which a contiguous
+//     split cannot give when all workgroups are resident at once.  Otherwise
+//     the pair is (2i, 2i+1);
 //   * the KV loop walks only the key tiles (BN = 64 keys) the mask can reach
-//     (prefix tiles + the band hull); K and V tiles are staged through LDS,
-//     double-buffered, one barrier per tile; each wavefront classifies the tile
-//     against its own rows and skips it (EMPTY), runs it unmasked (FULL) or
-//     with the per-element predicate (PARTIAL).
+//     (prefix tiles + the band hull).  K and V tiles go from HBM straight into
+//     LDS with global_load_lds_dwordx4 (no VGPR staging), three stages deep:
+//     tile t+2 is in flight while tile t is computed, one barrier per tile.
+//     Each wavefront classifies the tile against its own rows and skips it
+//     (EMPTY), runs it unmasked (FULL) or with the per-element predicate
+//     (PARTIAL).
 //
 // Matrix-core formulation (v_mfma_f32_32x32x16_bf16, fp32 accumulate)
 //   S^T[key, query] = K Q^T : A = K rows (ds_read_b128), B = Q rows kept in
@@ -28,11 +35,13 @@
 //     (i % 4) of the 8-byte rows addressed by lanes 4e + i/4, e = 0..3, so
 //     pointing lane s at V[k0 + s/4][d0 + 4 (s % 4)] hands lane i the four keys
 //     k0..k0+3 of column d0 + i -- exactly the key order of the B operand.
-//   LDS rows are padded instead of swizzled so that every fragment address is
-//   a per-lane base plus a compile-time offset: K rows are 2D+16 bytes apart
-//   (the eight rows of a ds_read_b128 phase land on distinct 16-byte bank
-//   groups), V rows 2D+32 bytes apart (the four rows x 32 bytes of one
-//   transposed-read group do).
+//   LDS tiles are dense rows of 2D bytes whose 16-byte chunks are XOR-swizzled
+//   (a DMA load fills 1 KB contiguously, so rows cannot be padded): K chunk c
+//   of row r sits in slot c ^ (r & 7), so the eight rows of a ds_read_b128
+//   phase hit distinct bank groups; V chunk c sits in slot c ^ 2 (r & 3), so
+//   the four rows x 32 bytes of one transposed-read group do.  With rows of
+//   a multiple of 128 bytes every fragment offset is a per-lane base XOR a
+//   compile-time constant.
 //   The softmax runs per 32-key block in the exp2 domain with a lazily moved
 //   reference max: the running max (and the O / l rescale) only changes when
 //   a block's max exceeds it by more than kRescaleLog2, so p <= 2^kRescaleLog2.
@@ -57,8 +66,6 @@ enum Norm : int { NORM_SOFTMAX = 0, NORM_SIGMOID = 1, NORM_RELU = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 constexpr int kBN = 64;
 
 struct FwdParams {
@@ -75,28 +82,61 @@ struct FwdParams {
   MaskSpec mask;              // original coordinates
   int32_t B, H;
   int32_t residues;           // dilation classes launched
-  int32_t n_qblk;             // query blocks per (b, h, residue)
+  int32_t n_pairs;            // row-block pairs per (b, h, residue 0)
+  int32_t zigzag;             // pair blocks (i, n-1-i) instead of (2i, 2i+1)
   int32_t n_wg;
   float scale, softcap, bias, post_scale;
 };
 
-// Query rows per wavefront (in units of 32) for each head dim.
+// Waves per SIMD the register budget targets: two at head_dim 64 (the
+// hardware then overlaps one wave's softmax with the other's MFMAs), one at
+// head_dim 128 (its O accumulator alone is 128 VGPRs).
 template <int D>
-struct TileCfg {
-  static constexpr int QB = (D == 64) ? 2 : 1;
+struct Occupancy {
+  static constexpr int value = D == 64 ? 2 : 1;
 };
 
-template <bool B>
-struct BoolTag {
-  static constexpr bool value = B;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int V>
+struct IntTag {
+  static constexpr int value = V;
 };
 
-// LDS row pitches (bytes) of the K and V tiles.
-template <int D>
-struct Pitch {
-  static constexpr int K = 2 * D + 16;
-  static constexpr int V = 2 * D + 32;
+// LDS stages of the K/V pipeline: 3 (tile t+2 in flight while t is computed)
+// for 4-wavefront workgroups, 2 for 2-wavefront ones so that four of them fit
+// in a CU's 160 KB of LDS.
+template <int NW>
+struct Stages {
+  static constexpr int value = NW == 2 ? 2 : 3;
 };
+
+// 32-bit LDS address of a generic pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Two transposed 8-byte reads (rows r and r+8 of one 16-key chunk) for each of
+// two d-blocks, issued as one unit that waits for its own completion.  Issued
+// through asm because the compiler treats the ds_read_tr intrinsic as aliasing
+// the in-flight LDS DMA and would otherwise wait for every outstanding global
+// load before it.
+template <int RP, int DB_OFF>
+__device__ __forceinline__ void v_read_tr2(uint32_t a0, uint32_t a1, i16x4_t& lo0, i16x4_t& hi0, i16x4_t& lo1,
+                                           i16x4_t& hi1) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4\n"
+      "ds_read_b64_tr_b16 %1, %4 offset:%6\n"
+      "ds_read_b64_tr_b16 %2, %5\n"
+      "ds_read_b64_tr_b16 %3, %5 offset:%6\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(lo0), "=&v"(hi0), "=&v"(lo1), "=&v"(hi1)
+      : "v"(a0), "v"(a1), "n"(8 * RP));
+}
+
+// Swizzled 16-byte slot of chunk c of row r in the K and V tiles.
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 7); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ (2 * (r & 3)); }
 
 // Hardware dispatches workgroup x to XCD x % 8.  Renumber so each XCD runs a
 // contiguous range of logical workgroups (the query blocks of the same heads
@@ -132,40 +172,54 @@ __device__ __forceinline__ bf16x2_t pack2(float a, float b) {
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) { return __builtin_bit_cast(uint32_t, pack2(a, b)); }
 
-template <int D, int QB, int NORM, bool ALIBI, bool SOFTCAP>
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p) {
+template <int D, int NW, int NORM, bool ALIBI, bool SOFTCAP>
+__global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(const FwdParams p) {
   constexpr int BN = kBN;
-  constexpr int QW = 32 * QB;        // query rows per wavefront
-  constexpr int BM = kWaves * QW;    // query rows per workgroup
+  constexpr int NT = NW * 64;        // threads per workgroup
+  constexpr int QB = 2;              // 32-row query blocks per wavefront (one per row block)
+  constexpr int BMH = NW * 32;       // rows per row block
   constexpr int KB = BN / 32;        // 32-key blocks per tile
   constexpr int DK = D / 16;         // k-steps of the QK^T MFMA
   constexpr int DB = D / 32;         // 32-row d blocks of O^T
   constexpr int DQ = D / 8;          // 16-byte chunks per K/V row
-  constexpr int NLD = BN * DQ / kThreads;  // 16-byte chunks per thread per tile (each of K, V)
-  constexpr int KP = Pitch<D>::K, VP = Pitch<D>::V;
-  constexpr int K_BYTES = BN * KP;
-  constexpr int STAGE_BYTES = K_BYTES + BN * VP;  // K tile + V tile
-  static_assert(NLD >= 1, "tile too small for the workgroup");
+  constexpr int RP = 2 * D;          // LDS row pitch (bytes)
+  constexpr int NDMA = BN * DQ / NT; // 1 KB DMA loads per wavefront per tile (each of K, V)
+  constexpr int K_BYTES = BN * RP;
+  constexpr int STAGE_BYTES = 2 * K_BYTES;  // K tile + V tile
+  static_assert(NDMA >= 1 && BN * DQ % NT == 0, "tile does not split into whole DMA loads");
+  static_assert(RP % 128 == 0, "rows must be whole multiples of 128 bytes for the XOR offsets");
   constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
 
-  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE_BYTES];
+  constexpr int NS = Stages<NW>::value;
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, lh = lane >> 5;
 
-  // ---- workgroup -> (batch, head, residue, query block) --------------------
+  // ---- workgroup -> (batch, head, residue, row-block pair) -----------------
   const int L = xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = L / p.n_qblk;
-  const int qblk = p.n_qblk - 1 - (L % p.n_qblk);  // heaviest (last) rows first
+  const int bhr = L / p.n_pairs;
+  const int pr = L % p.n_pairs;
   const int r = bhr % p.residues;
   const int bh = bhr / p.residues;
   const int h = bh % p.H, b = bh / p.H;
   const MaskGeom g = residue_geom(p.mask, r);
-  const int q0 = qblk * BM;
-  if (q0 >= g.S) return;  // whole workgroup, before any barrier
+  const int nblk = (g.S + BMH - 1) / BMH;  // row blocks of this residue
+  int blk0, blk1;
+  if (p.zigzag) {
+    blk0 = pr;
+    blk1 = nblk - 1 - pr;
+    if (blk1 < blk0) return;  // whole workgroup, before any barrier
+    if (blk1 == blk0) blk1 = -1;
+  } else {
+    blk0 = 2 * pr;
+    blk1 = 2 * pr + 1;
+    if (blk0 >= nblk) return;
+    if (blk1 >= nblk) blk1 = -1;
+  }
 
   const int dil = p.mask.dil;
   const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
@@ -208,18 +262,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
   const float post = kRawRelu ? p.post_scale * c1 : p.post_scale;
 
   // ---- wavefront rows, Q fragments, per-row key intervals -------------------
-  const int iw0 = q0 + wave * QW;
-  const bool wave_valid = iw0 < g.S;
-  const int wa = iw0, wb = imin32(iw0 + QW - 1, g.S - 1);
+  int row0[QB];      // first row of this wavefront's 32-row query block qb
+  bool valid[QB];
+  row0[0] = blk0 * BMH + 32 * wave;
+  row0[1] = (blk1 >= 0 ? blk1 : blk0) * BMH + 32 * wave;
+  valid[0] = row0[0] < g.S;
+  valid[1] = blk1 >= 0 && row0[1] < g.S;
 
   bf16x8_t qf[QB][DK];
-  int jl[QB], jh[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const int i = iw0 + 32 * qb + lq;
-    const bool ok = i < g.S;
-    jl[qb] = key_lo(g, i);
-    jh[qb] = key_hi(g, i);
+    const int i = row0[qb] + lq;
+    const bool ok = valid[qb] && i < g.S;
     const uint16_t* src = qh + (int64_t)(ok ? i : 0) * qrs + 8 * lh;
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
@@ -230,32 +284,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
   }
 
   // ---- KV tiles this workgroup visits ---------------------------------------
-  const TileRange tr = tile_range(g, q0, imin32(q0 + BM - 1, g.S - 1), BN);
+  const TileRange tr = tile_range(g, blk0 * BMH, imin32((blk1 >= 0 ? blk1 : blk0) * BMH + BMH - 1, g.S - 1), BN);
   const int ntiles = tr.n_pre + tr.n2;
 
-  // Global -> VGPR -> LDS staging.  Thread t moves chunks c = t + 256 n of each
-  // tile (row c / DQ, chunk c % DQ); rows past the end re-read the last row
-  // (finite values; the mask gives their scores p = 0).
-  u32x4_t kreg[NLD], vreg[NLD];
-  auto load_tile = [&](int jt0) {
+  // Global -> LDS DMA.  Load n of wavefront w fills LDS chunks
+  // [(n NW + w) 64, +64) of the K (or V) tile: lane l moves the 16-byte chunk
+  // that belongs in slot (pos % DQ) of row pos / DQ, i.e. logical chunk
+  // slot ^ swizzle(row).  Rows past the end re-read the last row (finite
+  // values; the mask gives their scores p = 0).
+  auto issue_tile = [&](int jt0, int stage) {
+    char* kst = lds + stage * STAGE_BYTES;
 #pragma unroll
-    for (int n = 0; n < NLD; ++n) {
-      const int c = tid + kThreads * n;
-      const int row = c / DQ, ch = c % DQ;
+    for (int n = 0; n < NDMA; ++n) {
+      const int pos = (n * NW + wave) * 64 + lane;
+      const int row = pos / DQ, slot = pos % DQ;
       const int j = imin32(jt0 + row, g.S - 1);
-      kreg[n] = *(const u32x4_t*)(kh + (int64_t)j * krs + 8 * ch);
-      vreg[n] = *(const u32x4_t*)(vh + (int64_t)j * vrs + 8 * ch);
-    }
-  };
-  auto store_tile = [&](int stage) {
-    char* ks_ = lds + stage * STAGE_BYTES;
-    char* vs_ = ks_ + K_BYTES;
-#pragma unroll
-    for (int n = 0; n < NLD; ++n) {
-      const int c = tid + kThreads * n;
-      const int row = c / DQ, ch = c % DQ;
-      *(u32x4_t*)(ks_ + row * KP + 16 * ch) = kreg[n];
-      *(u32x4_t*)(vs_ + row * VP + 16 * ch) = vreg[n];
+      const char* lbase = kst + (n * NW + wave) * 1024;
+      __builtin_amdgcn_global_load_lds(kh + (int64_t)j * krs + 8 * k_slot(row, slot), (lds_void_t*)lbase, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vh + (int64_t)j * vrs + 8 * v_slot(row, slot),
+                                       (lds_void_t*)(lbase + K_BYTES), 16, 0, 0);
     }
   };
 
@@ -274,16 +321,21 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
     l_run[qb] = 0.f;
   }
 
-  // Per-lane LDS byte offsets; every fragment is at a compile-time distance.
-  // K fragment (kb, kk): row 32 kb + lq, elements 16 kk + 8 lh .. +7.
-  const int k_lane = lq * KP + 16 * lh;
+  // Per-lane LDS byte offsets.  K fragment (kb, kk): row 32 kb + lq, chunk
+  // 2 kk + lh -> byte (32 kb) RP + [k_lane ^ 32 kk].
+  const int k_lane = lq * RP + 16 * k_slot(lq, lh);
   // V transposed read (c, rr, db): lane (group g16, slot s16) addresses row
-  // 16 c + 8 rr + 4 (g16 / 2) + s16 / 4, elements 32 db + 16 (g16 % 2) + 4 (s16 % 4) .. +3.
+  // 16 c + 8 rr + 4 (g16 / 2) + s16 / 4 and elements 32 db + 16 (g16 % 2) +
+  // 4 (s16 % 4) .. +3, i.e. byte (16 c + 8 rr) RP + [v_lane ^ 64 db].
   const int g16 = lane >> 4, s16 = lane & 15;
-  const int v_lane = K_BYTES + (4 * (g16 >> 1) + (s16 >> 2)) * VP + 2 * (16 * (g16 & 1) + 4 * (s16 & 3));
+  const int v_row = 4 * (g16 >> 1) + (s16 >> 2);
+  const int v_lane = K_BYTES + v_row * RP + 16 * v_slot(v_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
 
-  // One 32-key block of one tile for this wavefront.
-  auto key_block = [&](const char* St, int jt0, int kb, bool masked) {
+  // One 32-key block of one tile for this wavefront.  ACT (bit qb) selects
+  // the query blocks that see any key of the tile; masked[qb] selects the
+  // per-element predicate for a block the tile only partly covers.
+  auto key_block = [&](const char* St, int jt0, int kb, const bool* masked, auto act_tag) {
+    constexpr int ACT = decltype(act_tag)::value;
     f32x16_t sacc[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
@@ -293,17 +345,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
     // S^T = K Q^T for keys 32 kb .. 32 kb + 31
 #pragma unroll
     for (int kk = 0; kk < DK; ++kk) {
-      const bf16x8_t a = *(const bf16x8_t*)(St + k_lane + (32 * kb * KP + 32 * kk));
+      const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
-        sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], sacc[qb], 0, 0, 0);
+        if ((ACT >> qb) & 1)  // constant once the qb loop is unrolled
+          sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], sacc[qb], 0, 0, 0);
     }
 
     // score modifier -> t (in place)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      if constexpr (!kPlainSoftmax && !kRawRelu) {
-        const int i = iw0 + 32 * qb + lq;
+      if (!kPlainSoftmax && !kRawRelu && ((ACT >> qb) & 1)) {
+        const int i = row0[qb] + lq;
         const int jbase = jt0 + 32 * kb + 4 * lh;
         const float ksb = ALIBI ? ks * (float)(jbase - i) + k0 : k0;
 #pragma unroll
@@ -324,11 +377,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
       }
     }
     // mask (PARTIAL tiles only): softmax/ReLU -> -inf, sigmoid input -> +inf; all give p = 0
-    if (masked) {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
+      if (((ACT >> qb) & 1) && masked[qb]) {
+        // the row's key interval is recomputed here rather than kept live
+        const int i = row0[qb] + lq;
         const int jbase = jt0 + 32 * kb + 4 * lh;
-        const int vlo = jl[qb] - jbase, vhi = jh[qb] - jbase, vpre = g.prefix - jbase;
+        const int vlo = key_lo(g, i) - jbase, vhi = key_hi(g, i) - jbase, vpre = g.prefix - jbase;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int rc = 8 * (e >> 2) + (e & 3);
@@ -342,6 +397,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
     uint32_t pk[QB][8];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
+      if (!((ACT >> qb) & 1)) continue;
       if constexpr (NORM == NORM_SOFTMAX) {
         float mx = sacc[qb][0];
 #pragma unroll
@@ -399,50 +455,83 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
       bf16x8_t pf[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        const u32x4_t w = {pk[qb][4 * half], pk[qb][4 * half + 1], pk[qb][4 * half + 2], pk[qb][4 * half + 3]};
-        pf[qb] = __builtin_bit_cast(bf16x8_t, w);
+        if ((ACT >> qb) & 1) {
+          const u32x4_t w = {pk[qb][4 * half], pk[qb][4 * half + 1], pk[qb][4 * half + 2], pk[qb][4 * half + 3]};
+          pf[qb] = __builtin_bit_cast(bf16x8_t, w);
+        }
       }
+      static_assert(DB % 2 == 0, "d-blocks are read in pairs");
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const char* vp = St + v_lane + (16 * c * VP + 64 * db);
-        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vp);
-        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vp + 8 * VP));
+      for (int db = 0; db < DB; db += 2) {
+        const uint32_t va = lds_addr(St + 16 * c * RP) + (v_lane ^ (64 * db));
+        const uint32_t vb = lds_addr(St + 16 * c * RP) + (v_lane ^ (64 * (db + 1)));
+        i16x4_t lo0, hi0, lo1, hi1;
+        v_read_tr2<RP, 0>(va, vb, lo0, hi0, lo1, hi1);
         typedef short i16x8_t __attribute__((ext_vector_type(8)));
-        const i16x8_t av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, av);
+        const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo0, hi0, 0, 1, 2, 3, 4, 5, 6, 7));
+        const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo1, hi1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb)
-          oacc[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[qb], oacc[db][qb], 0, 0, 0);
+        for (int qb = 0; qb < QB; ++qb) {
+          if ((ACT >> qb) & 1) {
+            oacc[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf[qb], oacc[db][qb], 0, 0, 0);
+            oacc[db + 1][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf[qb], oacc[db + 1][qb], 0, 0, 0);
+          }
+        }
       }
     }
   };
 
-  auto tile_step = [&](const char* St, int jt0, bool masked) {
+  auto tile_step = [&](const char* St, int jt0, const bool* masked, auto act_tag) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) key_block(St, jt0, kb, masked);
+    for (int kb = 0; kb < KB; ++kb) key_block(St, jt0, kb, masked, act_tag);
   };
 
-  // ---- main loop: double-buffered LDS, one barrier per tile -----------------
-  if (ntiles > 0) {
-    load_tile(tile_at(tr, 0) * BN);
-    store_tile(0);
-  }
-  __syncthreads();
+  // ---- main loop: NS LDS stages, one barrier per tile ------------------------
+  // Iteration it waits for its own DMA of tile it (leaving the loads of the
+  // next NS-2 tiles in flight), then the barrier makes every wavefront's part
+  // of tile it visible and guarantees stage (it+NS-1) % NS -- last read in
+  // iteration it-1 -- is free for the DMA of tile it+NS-1.  The barrier is a
+  // bare s_barrier: a __syncthreads() fence would also wait for the loads
+  // still in flight.
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < ntiles) issue_tile(tile_at(tr, t) * BN, t);
   for (int it = 0; it < ntiles; ++it) {
     const int jt0 = tile_at(tr, it) * BN;
-    const bool has_next = it + 1 < ntiles;
-    if (has_next) load_tile(tile_at(tr, it + 1) * BN);
-    const char* St = lds + (it & 1) * STAGE_BYTES;
-    const int cls = wave_valid ? classify_tile(g, wa, wb, jt0, jt0 + BN - 1) : (int)TILE_EMPTY;
-    if (cls != TILE_EMPTY) tile_step(St, jt0, cls == TILE_PARTIAL);
-    if (has_next) store_tile((it + 1) & 1);
-    __syncthreads();
+    if constexpr (NS == 3) {
+      if (it + 1 < ntiles) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (it + NS - 1 < ntiles) issue_tile(tile_at(tr, it + NS - 1) * BN, (it + NS - 1) % NS);
+    const char* St = lds + (it % NS) * STAGE_BYTES;
+    int act = 0;
+    bool masked[QB];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int cls = valid[qb] ? classify_tile(g, row0[qb], imin32(row0[qb] + 31, g.S - 1), jt0, jt0 + BN - 1)
+                                : (int)TILE_EMPTY;
+      act |= (cls != TILE_EMPTY) << qb;
+      masked[qb] = cls == TILE_PARTIAL;
+    }
+    // Two code paths: both blocks, or only block 1 (the common case of a
+    // zigzag pair past the light block's diagonal).  A tile that only block 0
+    // sees runs the two-block path with block 1 fully masked.
+    if (act == 2) {
+      tile_step(St, jt0, masked, IntTag<2>{});
+    } else if (act != 0) {
+      masked[1] = masked[1] || act == 1;
+      tile_step(St, jt0, masked, IntTag<3>{});
+    }
   }
 
   // ---- epilogue: normalise and store ----------------------------------------
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const int i = iw0 + 32 * qb + lq;
+    const int i = row0[qb] + lq;
     float f;
     if constexpr (NORM == NORM_SOFTMAX) {
       const float lt = xhalf_sum(l_run[qb]);
@@ -450,7 +539,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(const FwdParams p
     } else {
       f = post;
     }
-    if (i < g.S) {
+    if (valid[qb] && i < g.S) {
       uint16_t* dst = oh + (int64_t)i * ors + 4 * lh;
 #pragma unroll
       for (int db = 0; db < DB; ++db)

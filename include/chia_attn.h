@@ -109,14 +109,14 @@ int chia_attn_fwd(const chia_attn_args* args, void* stream);
  * benchmark's FLOP accounting; the reference has no counterpart (its timer,
  * extra_bench.py:8-22, counts latency only). */
 typedef struct chia_attn_plan_info {
-  int32_t block_m;          /* queries per workgroup */
+  int32_t block_m;          /* query rows per workgroup (two row blocks) */
   int32_t block_n;          /* keys per KV tile */
-  int32_t wave_m;           /* queries per wavefront */
+  int32_t wave_m;           /* rows of one computed sub-tile (32) */
   int32_t waves;            /* wavefronts per workgroup */
   int64_t workgroups;       /* grid size */
-  int64_t tiles_total;      /* (query block, KV tile) pairs of the dense grid */
-  int64_t tiles_visited;    /* pairs the workgroups load (block_m x block_n) */
-  int64_t wave_tiles_visited; /* (wave rows, KV tile) pairs computed (wave_m x block_n) */
+  int64_t tiles_total;      /* (workgroup, KV tile) pairs of the dense grid */
+  int64_t tiles_visited;    /* (workgroup, KV tile) pairs loaded into LDS */
+  int64_t wave_tiles_visited; /* (32-row block, KV tile) pairs computed (wave_m x block_n) */
   int64_t wave_tiles_partial; /* of which need the per-element mask */
   int64_t pairs_visible;    /* exact number of visible (i, j) pairs over B*H */
   int32_t residues;         /* dilation classes the problem splits into */
