@@ -7,8 +7,8 @@ inputs already resident in HBM.  Prints ONE JSON line on stdout:
   variants     per variant: us/call (median of 3 event loops, extra_bench.py:8-22),
                cold-cache us/call, TFLOP/s (algorithmic, visited-tile, dense),
                fraction of the bf16 MFMA peak and of the HBM roofline
-  roofline     the dominant (slowest) variant's kernel, timed with HIP events
-               around each of its launches inside the timed steps
+  roofline     the dominant (slowest) variant's kernel, its average launch
+               duration from HIP events around back-to-back loops of it
   cpu_baseline the reference's eager path (restated in oracle/) on the host CPU,
                on a bounded sample, with the GPU output checked on that sample
 Everything else goes to stderr.
@@ -33,30 +33,35 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_name(op: str, D: int, params: dict) -> str:
+def kernel_name(op: str, B: int, H: int, S: int, D: int, params: dict) -> str:
+    """rocprofv3's name of the kernel instantiation a variant launches."""
+    from chia_proj_amd import plan
     from chia_proj_amd.accounting import core_plan_kwargs
 
-    kw = core_plan_kwargs(op, 16, params)
+    kw = core_plan_kwargs(op, H, params)
+    waves = plan(batch=B, heads=H, seqlen=S, head_dim=D, **kw)["waves"]
     norm = {"softmax": 0, "sigmoid": 1, "relu": 2}[kw.get("norm", "softmax")]
-    qb = 2 if D == 64 else 1
     al = "true" if kw["alibi"] else "false"
     sc = "true" if kw.get("softcap", 0) else "false"
-    return f"void chia::attn_fwd_kernel<{D}, {qb}, {norm}, {al}, {sc}>(chia::FwdParams)"
+    return f"void chia::attn_fwd_kernel<{D}, {waves}, {norm}, {al}, {sc}>(chia::FwdParams)"
 
 
-def load_traffic(kname: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/traffic.json), if recorded."""
+def load_traffic(suite: str, op: str, kname: str):
+    """HBM bytes per launch of `kname` on this suite's `op` workload, measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/traffic.json), if recorded."""
     path = REPO / "profiles" / "traffic.json"
     if not path.exists():
         return None
     try:
-        data = json.loads(path.read_text())
-    except (OSError, ValueError):
+        rec = json.loads(path.read_text()).get(suite, {}).get(op)
+    except (OSError, ValueError, AttributeError):
         return None
-    return data.get(kname)
+    if not rec or rec.get("kernel") != kname:
+        return None
+    return rec.get("bytes")
 
 
-def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16):
+def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16, reps: int = 5):
     """The reference's eager bf16 path (oracle.eager_bf16, extra_bench.py:37-50) on the
     host CPU for the first `sample_heads` head(s) of batch 0 of every variant, scaled
     to the full step; the same sample checks the GPU output against the fp32 oracle."""
@@ -78,7 +83,7 @@ def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16):
         p_sample = oracle.resolve_head_params(case.op, H, params, 0, sample_heads)
         oracle.eager_bf16(case.op, qs, ks, vs, **p_sample)  # warm-up
         ts = []
-        for _ in range(3):
+        for _ in range(reps):
             t0 = time.perf_counter_ns()
             ref_eager = oracle.eager_bf16(case.op, qs, ks, vs, **p_sample)
             ts.append((time.perf_counter_ns() - t0) * 1e-9)
@@ -101,7 +106,7 @@ def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16):
         "cores": threads,
         "kind": "port",
         "sample": (f"each variant's reference bf16 eager path (oracle.eager_bf16, extra_bench.py:37-50) on "
-                   f"{sample_heads} of the {cases[0].B * cases[0].H} (batch, head) slices, median of 3 after 1 "
+                   f"{sample_heads} of the {cases[0].B * cases[0].H} (batch, head) slices, median of {reps} after 1 "
                    f"warm-up, scaled by B*H/{sample_heads} to the full step; torch CPU threads={threads}"),
         "step_s_scaled": total_s,
         "gate_on_sample": checks,
@@ -119,6 +124,9 @@ def main() -> int:
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-calibration", action="store_true")
     ap.add_argument("--report", default="", help="also write the JSON line to this file")
+    ap.add_argument("--pmc-mode", action="store_true",
+                    help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
+                         "kernel that reads and writes 512 MiB, and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -155,39 +163,52 @@ def main() -> int:
     outputs = {c.name: calls[c.name]() for c in cases}
     torch.cuda.synchronize()
 
+    if args.pmc_mode:
+        flusher = CacheFlusher(nbytes=1 << 30, device=dev)
+        for c in cases:
+            for _ in range(2):
+                flusher()
+                calls[c.name]()
+        x = torch.empty(128 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        y = torch.empty_like(x)
+        flusher()
+        torch.add(x, 1.0, out=y)  # counter calibration: 512 MiB read, 512 MiB written
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_mode": True, "variants": [c.op for c in cases], "calibration_bytes": 2 * x.numel() * 4}))
+        return 0
+
     # ---- timed steps: W warm-up, then K steps bracketed by synchronize ----------
+    # Events only at the two ends: an event recorded between launches is a
+    # barrier packet that idles the GPU for a few microseconds.
     for _ in range(args.warmup):
         for c in cases:
             calls[c.name]()
     torch.cuda.synchronize()
-    ev = {c.name: [] for c in cases}
     t0 = time.perf_counter()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(args.steps):
         for c in cases:
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
             calls[c.name]()
-            e1.record()
-            ev[c.name].append((e0, e1))
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = start.elapsed_time(end) / args.steps
-    launch_us = {n: statistics.mean(a.elapsed_time(b) for a, b in pairs) * 1000.0 for n, pairs in ev.items()}
     log(f"[bench] {args.steps} steps: {step_ms:.3f} ms/step (event), wall {wall*1e3/args.steps:.3f} ms/step")
 
     # ---- per-variant: median of 3 event loops (reference timer), cold cache ----
+    # Each loop runs one variant back to back between two events, so the
+    # per-launch average is the kernel's own duration (rocprofv3 agrees).
     flusher = None if args.no_cold else CacheFlusher(device=dev)
     variants = {}
+    launch_us = {}
     for c in cases:
         us = median_us(calls[c.name])
         r = rates(works[c.name], us)
+        launch_us[c.name] = us
         row = {
             "us": round(us, 2),
-            "launch_us_in_steps": round(launch_us[c.name], 2),
             "tflops_alg": round(r["tflops_alg"], 2),
             "tflops_visited": round(r["tflops_visited"], 2),
             "tflops_dense": round(r["tflops_dense"], 2),
@@ -209,18 +230,18 @@ def main() -> int:
             + (f"cold {row['cold_us']:.1f} us" if "cold_us" in row else ""))
     del flusher
 
-    # ---- dominant kernel roofline (HIP events inside the timed steps) ----------
+    # ---- dominant kernel roofline (HIP events around its back-to-back loops) ----
     dom = max(cases, key=lambda c: launch_us[c.name])
     w = works[dom.name]
     avg = launch_us[dom.name]
-    kname = kernel_name(dom.op, dom.D, inputs[dom.name][3])
+    kname = kernel_name(dom.op, dom.B, dom.H, dom.S, dom.D, inputs[dom.name][3])
     if w["bound"] == "mfma":
         achieved, peak, unit, per_launch = w["flops_alg"] / (avg * 1e-6) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", w["flops_alg"]
     else:
         achieved, peak, unit, per_launch = w["bytes"] / (avg * 1e-6) / 1e9, PEAK_HBM_GBPS, "GB/s", w["bytes"]
     roofline = {
         "bound": w["bound"], "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-        "frac": round(achieved / peak, 4), "traffic": load_traffic(kname),
+        "frac": round(achieved / peak, 4), "traffic": load_traffic(args.suite, dom.op, kname),
         "kernel": kname, "variant": dom.op, "avg_launch_us": round(avg, 2),
         "algorithmic_per_launch": per_launch,
     }

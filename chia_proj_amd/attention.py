@@ -11,6 +11,7 @@ leaves synchronisation to the caller, extra_bench.py:12,19).
 from __future__ import annotations
 
 import math
+import threading
 from collections import OrderedDict
 from typing import Optional, Sequence, Union
 
@@ -23,6 +24,29 @@ PerHead = Union[None, torch.Tensor, Sequence[float]]
 SUPPORTED_HEAD_DIMS = (64, 128)
 _VEC_CACHE_MAX = 64
 _vec_cache: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+_ARGS_CACHE_MAX = 256
+_tls = threading.local()
+
+
+def _args_cache() -> "OrderedDict[tuple, tuple]":
+    cache = getattr(_tls, "args", None)
+    if cache is None:
+        cache = _tls.args = OrderedDict()
+    return cache
+
+
+def _head_key(vals: PerHead):
+    """Cache key of a per-head parameter: device tensors by identity of storage
+    (their values are read by the kernel at every call), host values by content."""
+    if vals is None:
+        return None
+    if isinstance(vals, torch.Tensor):
+        if vals.device.type == "cuda":
+            if vals.dtype != torch.float32 or not vals.is_contiguous():
+                raise TypeError("converted device vectors are not cached")  # caller takes the full path
+            return ("dev", vals.data_ptr(), tuple(vals.shape))
+        return ("host", tuple(vals.detach().reshape(-1).tolist()))
+    return ("host", tuple(float(x) for x in vals))
 
 
 def _per_head_vector(vals: PerHead, heads: int, device: torch.device, name: str,
@@ -103,6 +127,35 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
     softcap * tanh(s / softcap) when softcap > 0.
     norm: "softmax" | "sigmoid" (sigmoid(s + bias) * post_scale) | "relu" (relu(s) * post_scale).
     """
+    # Fast path: a call with the same shapes, layouts and parameters as an
+    # earlier one reuses its validated argument struct and per-head vectors;
+    # only the data pointers (and their alignment) are new.
+    try:
+        key = (q.shape, q.dtype, k.dtype, v.dtype, q.device, q.stride(), k.shape, k.stride(), v.shape, v.stride(),
+               k.device, v.device, None if out is None else (out.shape, out.dtype, out.device, out.stride()),
+               norm, causal, window, dilation, block, prefix, scale, softcap, bias, post_scale,
+               _head_key(head_scale), _head_key(alibi_slopes))
+    except (AttributeError, TypeError):
+        key = None
+    cache = _args_cache()
+    entry = cache.get(key) if key is not None else None
+    if entry is not None:
+        a, hs, sl = entry
+        o = torch.empty_like(q) if out is None else out
+        ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr())
+        if not (ptrs[0] | ptrs[1] | ptrs[2] | ptrs[3]) & 15:
+            a.q, a.k, a.v, a.o = ptrs
+            # device fp32 vectors are passed as they are (their values may change
+            # between calls); host values were copied to the device once
+            if hs is not None:
+                a.head_scale = (head_scale if isinstance(head_scale, torch.Tensor) and head_scale.is_cuda
+                                else hs).data_ptr()
+            if sl is not None:
+                a.alibi_slopes = (alibi_slopes if isinstance(alibi_slopes, torch.Tensor) and alibi_slopes.is_cuda
+                                  else sl).data_ptr()
+            _lib.fwd(a, torch.cuda.current_stream(q.device).cuda_stream)
+            return o
+
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
@@ -155,6 +208,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
     with torch.cuda.device(q.device):
         stream = torch.cuda.current_stream(q.device).cuda_stream
         _lib.fwd(a, stream)
+    # Cache the validated call when the tensors needed no layout change and a
+    # fresh output would get the same strides as this one.
+    if key is not None and q_ is q and k_ is k and v_ is v and (out is not None or o.stride() == q.stride()):
+        cache[key] = (a, hs, sl)
+        if len(cache) > _ARGS_CACHE_MAX:
+            cache.popitem(last=False)
     return o
 
 

@@ -79,8 +79,12 @@ Geometry geometry_of(const MaskSpec& m, int64_t batch, int64_t heads) {
   geo.zigzag = zigzag_of(m) ? 1 : 0;
   const int32_t s0 = residue_geom(m, 0).S;  // longest residue class
   // 4 wavefronts share each K/V tile among more rows; fall back to 2 when
-  // that leaves fewer than two workgroups per CU.
+  // that leaves fewer than two workgroups per CU.  Windowed or block masks
+  // always use 2: their key range per workgroup is the window plus the
+  // workgroup's rows, so smaller workgroups visit fewer partly-masked tiles.
+  const bool banded = m.hi < kInf || m.blk > 0;
   for (int waves : {4, 2}) {
+    if (waves == 4 && banded) continue;
     geo.waves = waves;
     geo.rows = 32 * waves;
     const int64_t nblk = (s0 + geo.rows - 1) / geo.rows;

@@ -1,0 +1,156 @@
+"""CPU tests of the C ABI (include/chia_attn.h) -- no GPU calls.
+
+The host-only entry points (chia_attn_plan, chia_attn_tile_map,
+chia_attn_query_intervals) run the same mask functions the kernel runs
+(chia_proj_amd/csrc/mask.h), so checking them against the oracle's masks pins
+the kernel's mask reduction, tile classification and FLOP accounting on the CPU.
+"""
+import ctypes
+import itertools
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from chia_proj_amd import _lib, make_args
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "chia_attn.h"
+
+
+def test_library_exports_every_declared_symbol(lib_built):
+    text = HEADER.read_text()
+    declared = set(re.findall(r"\b(chia_attn_[a-z_]+)\s*\(", text))
+    assert declared == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib_built, name), name
+
+
+def _c_struct_fields(text, name):
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        names = decl.split()[-1] if "," not in decl else decl
+        for part in re.split(r",", decl):
+            tok = part.strip().split()[-1].lstrip("*")
+            fields.append(re.sub(r"\[.*\]", "", tok))
+    return fields
+
+
+@pytest.mark.parametrize("cname,pyclass", [("chia_attn_args", _lib.AttnArgs), ("chia_attn_plan_info", _lib.PlanInfo)])
+def test_ctypes_mirrors_header_struct(cname, pyclass):
+    fields = _c_struct_fields(HEADER.read_text(), cname)
+    assert fields == [f[0] for f in pyclass._fields_]
+
+
+def test_status_strings_and_version(lib_built):
+    assert lib_built.chia_attn_abi_version() == _lib.ABI_VERSION
+    for st in (0, -1, -2, -3, -4, -5, -6, -7, -8):
+        assert _lib.status_string(st)
+    assert "unknown" in _lib.status_string(-99)
+
+
+def _plan_status(**kw):
+    a = make_args(batch=1, heads=1, seqlen=128, head_dim=64)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    info = _lib.PlanInfo()
+    return _lib.lib().chia_attn_plan(ctypes.byref(a), ctypes.byref(info))
+
+
+def test_validation_codes(lib_built):
+    assert _plan_status() == 0
+    assert _plan_status(head_dim=96) == -3
+    assert _plan_status(seqlen=0) == -2
+    assert _plan_status(batch=0) == -2
+    assert _plan_status(dilation=0) == -4
+    assert _plan_status(window=-1) == -4
+    assert _plan_status(dilation=2, prefix=4) == -4
+    assert _plan_status(scale=0.0) == -5
+    assert _plan_status(scale=float("nan")) == -5
+    assert _plan_status(softcap=-1.0) == -5
+    assert _plan_status(norm=7) == -6
+    assert _plan_status(struct_size=12) == -8
+    a = make_args(batch=1, heads=1, seqlen=128, head_dim=64)
+    a.reserved[3] = 1
+    assert lib_built.chia_attn_plan(ctypes.byref(a), ctypes.byref(_lib.PlanInfo())) == -8
+
+
+def test_fwd_rejects_bad_arguments_without_launching(lib_built):
+    # null tensors and misaligned pointers are host-side errors: no GPU is touched
+    a = make_args(batch=1, heads=1, seqlen=64, head_dim=64)
+    assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -1
+    a.q = a.k = a.v = a.o = 0x1000
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = 64 * 64, 64 * 64, 64
+    a.o = 0x1008  # not 16-byte aligned
+    assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -7
+    a.o = 0x1000
+    a.q_stride[2] = 60  # row stride not a multiple of 8 elements
+    assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -7
+    assert lib_built.chia_attn_fwd(None, None) == -1
+
+
+MASKS = [
+    dict(causal=c, window=w, dilation=d, block=b, prefix=p)
+    for c, w, d, b, p in itertools.product([True, False], [0, 5, 64, 300], [1, 2, 3], [0, 33, 128], [0, 40])
+    if not (d > 1 and p)
+]
+
+
+@pytest.mark.parametrize("S", [1, 63, 200, 513])
+def test_plan_pairs_match_oracle_mask(S, lib_built):
+    for kw in MASKS:
+        a = make_args(batch=2, heads=3, seqlen=S, head_dim=64, **kw)
+        got = _lib.plan(a)["pairs_visible"]
+        want = 6 * oracle.visible_mask(S, **kw).sum().item()
+        assert got == want, (S, kw)
+
+
+@pytest.mark.parametrize("S", [77, 300, 700])
+def test_intervals_and_tile_classes_match_oracle(S, lib_built):
+    for kw in MASKS:
+        a = make_args(batch=1, heads=1, seqlen=S, head_dim=64, **kw)
+        full = oracle.visible_mask(S, **kw).numpy()
+        dil = kw["dilation"]
+        for r in range(min(dil, S)):
+            sub = full[r::dil, r::dil]
+            n = sub.shape[0]
+            # pairs across residue classes are never visible when dilation > 1
+            if dil > 1:
+                off = full.copy()
+                off[r::dil, r::dil] = False
+                assert not off[r::dil].any()
+            jlo, jhi, pre = _lib.query_intervals(a, r, n)
+            jj = np.arange(n)
+            rebuilt = (jj[None, :] < pre) | ((jj[None, :] >= jlo[:, None]) & (jj[None, :] <= jhi[:, None]))
+            assert (rebuilt == sub).all(), (kw, r)
+            for rows in (32, 64, 128):
+                tm = _lib.tile_map(a, r, rows)
+                for qb, kt in itertools.product(range(tm.shape[0]), range(tm.shape[1])):
+                    blk = sub[qb * rows:(qb + 1) * rows, kt * 64:(kt + 1) * 64]
+                    if tm[qb, kt] == 0:
+                        assert not blk.any(), (kw, r, rows, qb, kt)
+                    elif tm[qb, kt] == 1:
+                        assert blk.shape[1] == 64 and blk.all(), (kw, r, rows, qb, kt)
+
+
+def test_plan_geometry(lib_built):
+    # causal without a window pairs row blocks (i, n-1-i); every pair is one workgroup
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, causal=True))
+    assert p["waves"] == 4 and p["block_m"] == 256 and p["workgroups"] == 4 * 16 * 8
+    # a window keeps 2-wavefront workgroups
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, causal=True, window=256))
+    assert p["waves"] == 2 and p["block_m"] == 128
+    # every visible pair is inside a computed 32 x 64 sub-tile
+    for kw in (dict(causal=True), dict(causal=True, window=256), dict(causal=False, block=256),
+               dict(causal=True, dilation=2, window=1024), dict(causal=True, prefix=1024)):
+        p = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=64, **kw))
+        assert p["wave_tiles_visited"] * 32 * 64 >= p["pairs_visible"]
+        assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]

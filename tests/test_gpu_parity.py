@@ -201,3 +201,21 @@ def test_errors_raise_not_abort():
         attention(z, z, z, dilation=0)
     with pytest.raises(ValueError):
         OPS["temp_perhead"](z, z, z, temperature=[1.0, -1.0])
+
+
+def test_cached_launch_path_follows_new_data():
+    """Repeated calls with one signature reuse the validated arguments: outputs must
+    follow new tensors and in-place updates of a device per-head vector."""
+    _say("[parity] cached launch path")
+    g = torch.Generator("cpu").manual_seed(13)
+    q, k, v, q2 = (torch.randn(1, 2, 300, 64, generator=g).to(torch.bfloat16) for _ in range(4))
+    qd, kd, vd, q2d = (t.to(DEV) for t in (q, k, v, q2))
+    t = torch.tensor([0.5, 2.0], device=DEV)
+    for qq, qqd, scale_mult in ((q, qd, 1.0), (q2, q2d, 1.0), (q2, q2d, 3.0)):
+        if scale_mult != 1.0:
+            t.mul_(scale_mult)  # same storage, new values
+        o = attention(qqd, kd, vd, causal=True, window=77, head_scale=t)
+        torch.cuda.synchronize()
+        r = oracle.attention_ref(qq, k, v, causal=True, window=77, head_scale=t.cpu())
+        res = gate.north_star_gate(r, o.float().cpu())
+        assert res.ok, res.stats
