@@ -116,22 +116,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-// Two transposed 8-byte reads (rows r and r+8 of one 16-key chunk) for each of
-// two d-blocks, issued as one unit that waits for its own completion.  Issued
-// through asm because the compiler treats the ds_read_tr intrinsic as aliasing
-// the in-flight LDS DMA and would otherwise wait for every outstanding global
-// load before it.
-template <int RP, int DB_OFF>
-__device__ __forceinline__ void v_read_tr2(uint32_t a0, uint32_t a1, i16x4_t& lo0, i16x4_t& hi0, i16x4_t& lo1,
-                                           i16x4_t& hi1) {
-  asm volatile(
-      "ds_read_b64_tr_b16 %0, %4\n"
-      "ds_read_b64_tr_b16 %1, %4 offset:%6\n"
-      "ds_read_b64_tr_b16 %2, %5\n"
-      "ds_read_b64_tr_b16 %3, %5 offset:%6\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(lo0), "=&v"(hi0), "=&v"(lo1), "=&v"(hi1)
-      : "v"(a0), "v"(a1), "n"(8 * RP));
+// One 16-byte-per-lane HBM -> LDS DMA load: lane l's chunk lands at
+// lds_base + 16 l.  Issued through asm so that the compiler does not track it:
+// it would otherwise treat every later LDS read as aliasing the transfer and
+// wait for all loads in flight.  The kernel orders the transfers itself with
+// explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_base) : "memory");
 }
 
 // Swizzled 16-byte slot of chunk c of row r in the K and V tiles.
@@ -299,10 +290,9 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       const int pos = (n * NW + wave) * 64 + lane;
       const int row = pos / DQ, slot = pos % DQ;
       const int j = imin32(jt0 + row, g.S - 1);
-      const char* lbase = kst + (n * NW + wave) * 1024;
-      __builtin_amdgcn_global_load_lds(kh + (int64_t)j * krs + 8 * k_slot(row, slot), (lds_void_t*)lbase, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vh + (int64_t)j * vrs + 8 * v_slot(row, slot),
-                                       (lds_void_t*)(lbase + K_BYTES), 16, 0, 0);
+      const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
+      dma16(kh + (int64_t)j * krs + 8 * k_slot(row, slot), lbase);
+      dma16(vh + (int64_t)j * vrs + 8 * v_slot(row, slot), lbase + K_BYTES);
     }
   };
 
@@ -463,10 +453,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       static_assert(DB % 2 == 0, "d-blocks are read in pairs");
 #pragma unroll
       for (int db = 0; db < DB; db += 2) {
-        const uint32_t va = lds_addr(St + 16 * c * RP) + (v_lane ^ (64 * db));
-        const uint32_t vb = lds_addr(St + 16 * c * RP) + (v_lane ^ (64 * (db + 1)));
-        i16x4_t lo0, hi0, lo1, hi1;
-        v_read_tr2<RP, 0>(va, vb, lo0, hi0, lo1, hi1);
+        const char* va = St + 16 * c * RP + (v_lane ^ (64 * db));
+        const char* vb = St + 16 * c * RP + (v_lane ^ (64 * (db + 1)));
+        const i16x4_t lo0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)va);
+        const i16x4_t hi0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(va + 8 * RP));
+        const i16x4_t lo1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vb);
+        const i16x4_t hi1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vb + 8 * RP));
         typedef short i16x8_t __attribute__((ext_vector_type(8)));
         const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo0, hi0, 0, 1, 2, 3, 4, 5, 6, 7));
         const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo1, hi1, 0, 1, 2, 3, 4, 5, 6, 7));
