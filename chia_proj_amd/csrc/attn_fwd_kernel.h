@@ -98,9 +98,9 @@ struct Occupancy {
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int V>
-struct IntTag {
-  static constexpr int value = V;
+template <bool V>
+struct BoolTag {
+  static constexpr bool value = V;
 };
 
 // LDS stages of the K/V pipeline: 3 (tile t+2 in flight while t is computed)
@@ -116,13 +116,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-// One 16-byte-per-lane HBM -> LDS DMA load: lane l's chunk lands at
-// lds_base + 16 l.  Issued through asm so that the compiler does not track it:
+// One 16-byte-per-lane HBM -> LDS DMA load from sbase + voff (uniform base,
+// per-lane byte offset): lane l's chunk lands at lds_base + 16 l.  Issued through asm so that the compiler does not track it:
 // it would otherwise treat every later LDS read as aliasing the transfer and
 // wait for all loads in flight.  The kernel orders the transfers itself with
 // explicit vmcnt waits and barriers.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_base) : "memory");
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
 }
 
 // Swizzled 16-byte slot of chunk c of row r in the K and V tiles.
@@ -179,6 +179,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   constexpr int STAGE_BYTES = 2 * K_BYTES;  // K tile + V tile
   static_assert(NDMA >= 1 && BN * DQ % NT == 0, "tile does not split into whole DMA loads");
   static_assert(RP % 128 == 0, "rows must be whole multiples of 128 bytes for the XOR offsets");
+  static_assert(KB == 2, "a WIDE step covers the two key blocks of a tile");
   constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
 
@@ -281,19 +282,59 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // Global -> LDS DMA.  Load n of wavefront w fills LDS chunks
   // [(n NW + w) 64, +64) of the K (or V) tile: lane l moves the 16-byte chunk
   // that belongs in slot (pos % DQ) of row pos / DQ, i.e. logical chunk
-  // slot ^ swizzle(row).  Rows past the end re-read the last row (finite
-  // values; the mask gives their scores p = 0).
+  // slot ^ swizzle(row).  The per-lane byte offsets from the tile's first row
+  // are fixed; a tile adds its (uniform) row base.  Rows past the end re-read
+  // the last row (finite values; the mask gives their scores p = 0).
+  uint32_t k_dma[NDMA], v_dma[NDMA];
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int pos = (n * NW + wave) * 64 + lane;
+    const int row = pos / DQ, slot = pos % DQ;
+    k_dma[n] = (uint32_t)(2 * ((int64_t)row * krs + 8 * k_slot(row, slot)));
+    v_dma[n] = (uint32_t)(2 * ((int64_t)row * vrs + 8 * v_slot(row, slot)));
+  }
   auto issue_tile = [&](int jt0, int stage) {
     char* kst = lds + stage * STAGE_BYTES;
+    const uint16_t* kt = kh + (int64_t)jt0 * krs;
+    const uint16_t* vt = vh + (int64_t)jt0 * vrs;
+    if (jt0 + BN <= g.S) {
 #pragma unroll
-    for (int n = 0; n < NDMA; ++n) {
-      const int pos = (n * NW + wave) * 64 + lane;
-      const int row = pos / DQ, slot = pos % DQ;
-      const int j = imin32(jt0 + row, g.S - 1);
-      const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
-      dma16(kh + (int64_t)j * krs + 8 * k_slot(row, slot), lbase);
-      dma16(vh + (int64_t)j * vrs + 8 * v_slot(row, slot), lbase + K_BYTES);
+      for (int n = 0; n < NDMA; ++n) {
+        const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
+        dma16s(kt, k_dma[n], lbase);
+        dma16s(vt, v_dma[n], lbase + K_BYTES);
+      }
+    } else {
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) {
+        const int pos = (n * NW + wave) * 64 + lane;
+        const int row = pos / DQ, slot = pos % DQ;
+        const int rr = imin32(row, g.S - 1 - jt0);
+        const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
+        dma16s(kt, (uint32_t)(2 * ((int64_t)rr * krs + 8 * k_slot(row, slot))), lbase);
+        dma16s(vt, (uint32_t)(2 * ((int64_t)rr * vrs + 8 * v_slot(row, slot))), lbase + K_BYTES);
+      }
     }
+  };
+
+  // Tile classes: each query block's key hull [ulo, uhi] and common interval
+  // [ilo, ihi] (classify_tile with the row-dependent parts hoisted).
+  int c_ulo[QB], c_uhi[QB], c_ilo[QB], c_ihi[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int a = row0[qb], b = imin32(row0[qb] + 31, g.S - 1);
+    c_ulo[qb] = key_lo(g, a);
+    c_uhi[qb] = key_hi(g, b);
+    c_ilo[qb] = key_lo(g, b);
+    c_ihi[qb] = key_hi(g, a);
+  }
+  auto tile_class = [&](int qb, int c, int d) {
+    if (!valid[qb]) return (int)TILE_EMPTY;
+    const bool tail = d > g.S - 1;
+    if (!tail && d < g.prefix) return (int)TILE_FULL;
+    if (c_ulo[qb] > c_uhi[qb] || c > c_uhi[qb] || d < c_ulo[qb]) return c < g.prefix ? (int)TILE_PARTIAL : (int)TILE_EMPTY;
+    if (!tail && c >= c_ilo[qb] && d <= c_ihi[qb]) return (int)TILE_FULL;
+    return (int)TILE_PARTIAL;
   };
 
   // ---- accumulators ---------------------------------------------------------
@@ -321,111 +362,143 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   const int v_row = 4 * (g16 >> 1) + (s16 >> 2);
   const int v_lane = K_BYTES + v_row * RP + 16 * v_slot(v_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
 
-  // One 32-key block of one tile for this wavefront.  ACT (bit qb) selects
-  // the query blocks that see any key of the tile; masked[qb] selects the
-  // per-element predicate for a block the tile only partly covers.
-  auto key_block = [&](const char* St, int jt0, int kb, const bool* masked, auto act_tag) {
-    constexpr int ACT = decltype(act_tag)::value;
-    f32x16_t sacc[QB];
+  // One tile for this wavefront, as a set of 32 x 32 score blocks ("streams"):
+  //   PAIR (WIDE = false): four streams, query blocks {0, 1} x key blocks
+  //     {0, 1}; the K / V fragments of a key block serve both query blocks;
+  //   WIDE: two streams, query block 1 x key blocks {0, 1} -- a tile that only
+  //     block 1 sees (a zigzag pair past the light block's diagonal).
+  // All QK^T MFMAs of the tile are issued before the softmax needs their
+  // results, and each query block's row state (m, l) takes one joint update
+  // per tile, so the only branch between the first MFMA and the last one is
+  // the (rare) rescale.  masked[qb] selects the per-element predicate for a
+  // block the tile only partly covers.
+  auto tile_step = [&](const char* St, int jt0, const bool* masked, auto wide_tag) {
+    constexpr bool WIDE = decltype(wide_tag)::value;
+    constexpr int NSTR = WIDE ? 2 : 4;
+    auto qb_of = [](int st) { return WIDE ? 1 : (st & 1); };
+    auto kb_of = [](int st) { return WIDE ? st : (st >> 1); };
+    f32x16_t sacc[NSTR];
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
+    for (int st = 0; st < NSTR; ++st)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[qb][e] = 0.f;
+      for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
 
-    // S^T = K Q^T for keys 32 kb .. 32 kb + 31
+    // S^T = K Q^T, key block by key block
 #pragma unroll
-    for (int kk = 0; kk < DK; ++kk) {
-      const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
+    for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
-        if ((ACT >> qb) & 1)  // constant once the qb loop is unrolled
-          sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb][kk], sacc[qb], 0, 0, 0);
+      for (int kk = 0; kk < DK; ++kk) {
+        const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
+#pragma unroll
+        for (int st = 0; st < NSTR; ++st)
+          if (kb_of(st) == kb)
+            sacc[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[qb_of(st)][kk], sacc[st], 0, 0, 0);
+      }
     }
 
     // score modifier -> t (in place)
+    if constexpr (!kPlainSoftmax && !kRawRelu) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      if (!kPlainSoftmax && !kRawRelu && ((ACT >> qb) & 1)) {
-        const int i = row0[qb] + lq;
-        const int jbase = jt0 + 32 * kb + 4 * lh;
+      for (int st = 0; st < NSTR; ++st) {
+        const int i = row0[qb_of(st)] + lq;
+        const int jbase = jt0 + 32 * kb_of(st) + 4 * lh;
         const float ksb = ALIBI ? ks * (float)(jbase - i) + k0 : k0;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int rc = 8 * (e >> 2) + (e & 3);  // key offset of register e
-          const float qk = sacc[qb][e];
+          const float qk = sacc[st][e];
           float lin;
           if constexpr (ALIBI) lin = __builtin_fmaf(qk, kq, __builtin_fmaf(ks, (float)rc, ksb));
           else if constexpr (NORM == NORM_SIGMOID && !SOFTCAP) lin = __builtin_fmaf(qk, kq, k0);
           else lin = qk * kq;
           if constexpr (SOFTCAP) {
             const float u = __builtin_amdgcn_exp2f(lin);
-            sacc[qb][e] = __builtin_fmaf(__builtin_amdgcn_rcpf(1.0f + u), sc_a, sc_b);
+            sacc[st][e] = __builtin_fmaf(__builtin_amdgcn_rcpf(1.0f + u), sc_a, sc_b);
           } else {
-            sacc[qb][e] = lin;
+            sacc[st][e] = lin;
           }
         }
       }
     }
     // mask (PARTIAL tiles only): softmax/ReLU -> -inf, sigmoid input -> +inf; all give p = 0
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      if (((ACT >> qb) & 1) && masked[qb]) {
+    for (int st = 0; st < NSTR; ++st) {
+      if (masked[qb_of(st)]) {
         // the row's key interval is recomputed here rather than kept live
-        const int i = row0[qb] + lq;
-        const int jbase = jt0 + 32 * kb + 4 * lh;
+        const int i = row0[qb_of(st)] + lq;
+        const int jbase = jt0 + 32 * kb_of(st) + 4 * lh;
         const int vlo = key_lo(g, i) - jbase, vhi = key_hi(g, i) - jbase, vpre = g.prefix - jbase;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           const int rc = 8 * (e >> 2) + (e & 3);
           const bool vis = (rc < vpre) | ((rc >= vlo) & (rc <= vhi));
-          sacc[qb][e] = vis ? sacc[qb][e] : ((NORM == NORM_SIGMOID) ? INFINITY : -INFINITY);
+          sacc[st][e] = vis ? sacc[st][e] : ((NORM == NORM_SIGMOID) ? INFINITY : -INFINITY);
         }
       }
     }
 
-    // normaliser -> p, packed to bf16 pairs (pk[qb][w] holds registers 2w, 2w+1)
-    uint32_t pk[QB][8];
+    // normaliser -> p, packed to bf16 pairs (pk[st][w] holds registers 2w, 2w+1)
+    uint32_t pk[NSTR][8];
+    if constexpr (NORM == NORM_SOFTMAX) {
+      // joint row max over the tile's key blocks of each query block
+      float mq[QB] = {-INFINITY, -INFINITY};
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      if (!((ACT >> qb) & 1)) continue;
-      if constexpr (NORM == NORM_SOFTMAX) {
-        float mx = sacc[qb][0];
+      for (int st = 0; st < NSTR; ++st) {
+        float mx = sacc[st][0];
 #pragma unroll
-        for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[qb][e]);
-        mx = xhalf_max(mx);
+        for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+        mq[qb_of(st)] = fmaxf(mq[qb_of(st)], mx);
+      }
+      float m_new[QB];
+      bool moved = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        if (WIDE && qb == 0) continue;
+        float mx = xhalf_max(mq[qb]);
         if constexpr (kPlainSoftmax) mx = mx * kq;  // kq > 0
-        const float m_old = m_run[qb];
-        const float m_new = (mx > m_old + kRescaleLog2) ? mx : m_old;
-        if (__any(m_new != m_old)) {
-          const float alpha = (m_old == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_old - m_new);
+        m_new[qb] = (mx > m_run[qb] + kRescaleLog2) ? mx : m_run[qb];
+        moved |= m_new[qb] != m_run[qb];
+      }
+      if (__any(moved)) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          if (WIDE && qb == 0) continue;
+          const float alpha = (m_run[qb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new[qb]);
           l_run[qb] *= alpha;
 #pragma unroll
           for (int db = 0; db < DB; ++db)
 #pragma unroll
             for (int e = 0; e < 16; ++e) oacc[db][qb][e] *= alpha;
+          m_run[qb] = m_new[qb];
         }
-        m_run[qb] = m_new;
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      }
+#pragma unroll
+      for (int st = 0; st < NSTR; ++st) {
+        const int qb = qb_of(st);
+        const float m_use = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb];
         float ls = l_run[qb];
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
           float p0, p1;
           if constexpr (kPlainSoftmax) {
-            p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][2 * w], kq, -m_use));
-            p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][2 * w + 1], kq, -m_use));
+            p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, -m_use));
+            p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, -m_use));
           } else {
-            p0 = __builtin_amdgcn_exp2f(sacc[qb][2 * w] - m_use);
-            p1 = __builtin_amdgcn_exp2f(sacc[qb][2 * w + 1] - m_use);
+            p0 = __builtin_amdgcn_exp2f(sacc[st][2 * w] - m_use);
+            p1 = __builtin_amdgcn_exp2f(sacc[st][2 * w + 1] - m_use);
           }
           const bf16x2_t pb = pack2(p0, p1);
           ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);  // row sum of the bf16 weights
-          pk[qb][w] = __builtin_bit_cast(uint32_t, pb);
+          pk[st][w] = __builtin_bit_cast(uint32_t, pb);
         }
         l_run[qb] = ls;
-      } else {
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < NSTR; ++st) {
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
-          float p0 = sacc[qb][2 * w], p1 = sacc[qb][2 * w + 1];
+          float p0 = sacc[st][2 * w], p1 = sacc[st][2 * w + 1];
           if constexpr (NORM == NORM_SIGMOID) {
             p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p0));
             p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p1));
@@ -433,24 +506,17 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
             p0 = fmaxf(p0, 0.f);
             p1 = fmaxf(p1, 0.f);
           }
-          pk[qb][w] = __builtin_bit_cast(uint32_t, pack2(p0, p1));
+          pk[st][w] = __builtin_bit_cast(uint32_t, pack2(p0, p1));
         }
       }
     }
 
-    // O^T += V^T P^T over the two 16-key chunks of this block
+    // O^T += V^T P^T, 16-key chunk by chunk
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    static_assert(DB % 2 == 0, "d-blocks are read in pairs");
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int c = 2 * kb + half;
-      bf16x8_t pf[QB];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        if ((ACT >> qb) & 1) {
-          const u32x4_t w = {pk[qb][4 * half], pk[qb][4 * half + 1], pk[qb][4 * half + 2], pk[qb][4 * half + 3]};
-          pf[qb] = __builtin_bit_cast(bf16x8_t, w);
-        }
-      }
-      static_assert(DB % 2 == 0, "d-blocks are read in pairs");
+    for (int c = 0; c < 2 * KB; ++c) {
+      const int kb = c >> 1, half = c & 1;
 #pragma unroll
       for (int db = 0; db < DB; db += 2) {
         const char* va = St + 16 * c * RP + (v_lane ^ (64 * db));
@@ -459,23 +525,19 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
         const i16x4_t hi0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(va + 8 * RP));
         const i16x4_t lo1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vb);
         const i16x4_t hi1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vb + 8 * RP));
-        typedef short i16x8_t __attribute__((ext_vector_type(8)));
         const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo0, hi0, 0, 1, 2, 3, 4, 5, 6, 7));
         const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo1, hi1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          if ((ACT >> qb) & 1) {
-            oacc[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf[qb], oacc[db][qb], 0, 0, 0);
-            oacc[db + 1][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf[qb], oacc[db + 1][qb], 0, 0, 0);
-          }
+        for (int st = 0; st < NSTR; ++st) {
+          if (kb_of(st) != kb) continue;
+          const int qb = qb_of(st);
+          const u32x4_t w = {pk[st][4 * half], pk[st][4 * half + 1], pk[st][4 * half + 2], pk[st][4 * half + 3]};
+          const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, w);
+          oacc[db][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf, oacc[db][qb], 0, 0, 0);
+          oacc[db + 1][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf, oacc[db + 1][qb], 0, 0, 0);
         }
       }
     }
-  };
-
-  auto tile_step = [&](const char* St, int jt0, const bool* masked, auto act_tag) {
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) key_block(St, jt0, kb, masked, act_tag);
   };
 
   // ---- main loop: NS LDS stages, one barrier per tile ------------------------
@@ -504,19 +566,18 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     bool masked[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-      const int cls = valid[qb] ? classify_tile(g, row0[qb], imin32(row0[qb] + 31, g.S - 1), jt0, jt0 + BN - 1)
-                                : (int)TILE_EMPTY;
+      const int cls = tile_class(qb, jt0, jt0 + BN - 1);
       act |= (cls != TILE_EMPTY) << qb;
       masked[qb] = cls == TILE_PARTIAL;
     }
-    // Two code paths: both blocks, or only block 1 (the common case of a
-    // zigzag pair past the light block's diagonal).  A tile that only block 0
-    // sees runs the two-block path with block 1 fully masked.
+    // Two code paths: both blocks (PAIR), or only block 1 (WIDE: the common
+    // case of a zigzag pair past the light block's diagonal).  A tile that
+    // only block 0 sees runs the PAIR path with block 1 fully masked.
     if (act == 2) {
-      tile_step(St, jt0, masked, IntTag<2>{});
+      tile_step(St, jt0, masked, BoolTag<true>{});
     } else if (act != 0) {
       masked[1] = masked[1] || act == 1;
-      tile_step(St, jt0, masked, IntTag<3>{});
+      tile_step(St, jt0, masked, BoolTag<false>{});
     }
   }
 
