@@ -22,6 +22,7 @@ KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap);
 namespace {
 
 constexpr int64_t kMaxSeq = (int64_t)1 << 28;
+constexpr int64_t kMaxKvRowStride = (int64_t)1 << 25;  // elements between K/V rows the kernel steps over
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 bool stride_ok(const int64_t* s) { return s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
@@ -48,6 +49,10 @@ int validate(const chia_attn_args* a, bool need_tensors) {
     if (!stride_ok(a->q_stride) || !stride_ok(a->k_stride) || !stride_ok(a->v_stride) || !stride_ok(a->o_stride))
       return CHIA_ATTN_ERR_ALIGN;
     if (((uintptr_t)a->head_scale & 3u) || ((uintptr_t)a->alibi_slopes & 3u)) return CHIA_ATTN_ERR_ALIGN;
+    // K/V tile loads address a tile's rows with 32-bit byte offsets from the
+    // tile's first row: 64 rows x (seq stride x dilation) x 2 bytes < 2^32.
+    for (const int64_t* st : {a->k_stride, a->v_stride})
+      if (st[2] < 0 || st[2] * a->dilation >= kMaxKvRowStride) return CHIA_ATTN_ERR_SHAPE;
   }
   return CHIA_ATTN_OK;
 }
@@ -106,7 +111,8 @@ extern "C" const char* chia_attn_status_string(int status) {
   switch (status) {
     case CHIA_ATTN_OK: return "ok";
     case CHIA_ATTN_ERR_NULL: return "null argument, tensor or required per-head pointer";
-    case CHIA_ATTN_ERR_SHAPE: return "batch, heads and seqlen must be >= 1 (seqlen < 2^28)";
+    case CHIA_ATTN_ERR_SHAPE:
+      return "batch, heads and seqlen must be >= 1 (seqlen < 2^28); K/V seq strides in [0, 2^25 / dilation)";
     case CHIA_ATTN_ERR_HEAD_DIM: return "head_dim must be 64 or 128";
     case CHIA_ATTN_ERR_MASK: return "window, block and prefix must be >= 0, dilation >= 1, and prefix is not combinable with dilation > 1";
     case CHIA_ATTN_ERR_SCALE: return "scale must be finite and > 0; softcap finite and >= 0; bias, post_scale finite";

@@ -121,8 +121,15 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // it would otherwise treat every later LDS read as aliasing the transfer and
 // wait for all loads in flight.  The kernel orders the transfers itself with
 // explicit vmcnt waits and barriers.
+// The base is made explicitly wave-uniform (it is by construction) so that
+// it always lands in scalar registers.  readfirstlane returns int: each half
+// goes back through uint32_t so that the low word is not sign-extended.
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
+  const uint64_t v = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint64_t u = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u), "{m0}"(lds_base) : "memory");
 }
 
 // Swizzled 16-byte slot of chunk c of row r in the K and V tiles.

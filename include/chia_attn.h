@@ -47,7 +47,8 @@ enum chia_attn_norm {
 enum chia_attn_status {
   CHIA_ATTN_OK = 0,
   CHIA_ATTN_ERR_NULL = -1,          /* NULL args, tensor or required pointer */
-  CHIA_ATTN_ERR_SHAPE = -2,         /* batch/heads/seqlen < 1 or too large  */
+  CHIA_ATTN_ERR_SHAPE = -2,         /* batch/heads/seqlen < 1 or too large, or a K/V seq
+                                        stride < 0 or >= 2^25 / dilation elements      */
   CHIA_ATTN_ERR_HEAD_DIM = -3,      /* head_dim not in {64, 128}            */
   CHIA_ATTN_ERR_MASK = -4,          /* negative window/block/prefix, dilation < 1,
                                        or prefix > 0 with dilation > 1 */

@@ -94,6 +94,17 @@ def test_fwd_rejects_bad_arguments_without_launching(lib_built):
     a.o = 0x1000
     a.q_stride[2] = 60  # row stride not a multiple of 8 elements
     assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -7
+    a.q_stride[2] = 64
+    # K/V rows are addressed with 32-bit offsets within a tile: negative or
+    # huge sequence strides are rejected
+    a.k_stride[2] = -64
+    assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -2
+    a.k_stride[2] = 64
+    a.v_stride[2] = 1 << 25
+    assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -2
+    a.v_stride[2] = 1 << 24
+    a.dilation = 2
+    assert lib_built.chia_attn_fwd(ctypes.byref(a), None) == -2
     assert lib_built.chia_attn_fwd(None, None) == -1
 
 
