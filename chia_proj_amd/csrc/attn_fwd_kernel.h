@@ -428,18 +428,20 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       }
     }
     // mask (PARTIAL tiles only): softmax/ReLU -> -inf, sigmoid input -> +inf; all give p = 0
+    if (masked[0] || masked[1]) {
 #pragma unroll
-    for (int st = 0; st < NSTR; ++st) {
-      if (masked[qb_of(st)]) {
-        // the row's key interval is recomputed here rather than kept live
-        const int i = row0[qb_of(st)] + lq;
-        const int jbase = jt0 + 32 * kb_of(st) + 4 * lh;
-        const int vlo = key_lo(g, i) - jbase, vhi = key_hi(g, i) - jbase, vpre = g.prefix - jbase;
+      for (int st = 0; st < NSTR; ++st) {
+        if (masked[qb_of(st)]) {
+          // the row's key interval is recomputed here rather than kept live
+          const int i = row0[qb_of(st)] + lq;
+          const int jbase = jt0 + 32 * kb_of(st) + 4 * lh;
+          const int vlo = key_lo(g, i) - jbase, vhi = key_hi(g, i) - jbase, vpre = g.prefix - jbase;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int rc = 8 * (e >> 2) + (e & 3);
-          const bool vis = (rc < vpre) | ((rc >= vlo) & (rc <= vhi));
-          sacc[st][e] = vis ? sacc[st][e] : ((NORM == NORM_SIGMOID) ? INFINITY : -INFINITY);
+          for (int e = 0; e < 16; ++e) {
+            const int rc = 8 * (e >> 2) + (e & 3);
+            const bool vis = (rc < vpre) | ((rc >= vlo) & (rc <= vhi));
+            sacc[st][e] = vis ? sacc[st][e] : ((NORM == NORM_SIGMOID) ? INFINITY : -INFINITY);
+          }
         }
       }
     }
@@ -557,6 +559,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 #pragma unroll
   for (int t = 0; t < NS - 1; ++t)
     if (t < ntiles) issue_tile(tile_at(tr, t) * BN, t);
+  // Band tiles whose class is known without classifying (both blocks FULL,
+  // or block 0 done and block 1 FULL); everything else is classified.
+  const FastRanges fr = fast_ranges(g, row0[0], imin32(row0[0] + 31, g.S - 1), valid[0], row0[1],
+                                    imin32(row0[1] + 31, g.S - 1), valid[1], BN);
   for (int it = 0; it < ntiles; ++it) {
     const int jt0 = tile_at(tr, it) * BN;
     if constexpr (NS == 3) {
@@ -570,12 +576,19 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     if (it + NS - 1 < ntiles) issue_tile(tile_at(tr, it + NS - 1) * BN, (it + NS - 1) % NS);
     const char* St = lds + (it % NS) * STAGE_BYTES;
     int act = 0;
-    bool masked[QB];
+    bool masked[QB] = {false, false};
+    const int t = jt0 / BN;
+    if (it >= tr.n_pre && t >= fr.pf_lo && t <= fr.pf_hi) {
+      act = 3;
+    } else if (it >= tr.n_pre && t >= fr.wf_lo && t <= fr.wf_hi) {
+      act = 2;
+    } else {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int cls = tile_class(qb, jt0, jt0 + BN - 1);
-      act |= (cls != TILE_EMPTY) << qb;
-      masked[qb] = cls == TILE_PARTIAL;
+      for (int qb = 0; qb < QB; ++qb) {
+        const int cls = tile_class(qb, jt0, jt0 + BN - 1);
+        act |= (cls != TILE_EMPTY) << qb;
+        masked[qb] = cls == TILE_PARTIAL;
+      }
     }
     // Two code paths: both blocks (PAIR), or only block 1 (WIDE: the common
     // case of a zigzag pair past the light block's diagonal).  A tile that

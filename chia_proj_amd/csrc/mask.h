@@ -89,6 +89,37 @@ CHIA_HD int32_t classify_tile(const MaskGeom& g, int32_t a, int32_t b, int32_t c
   return TILE_PARTIAL;
 }
 
+// Band key tiles (index t, keys [bn t, bn t + bn - 1], t >= the prefix tiles)
+// whose classes for two query blocks [a0, b0], [a1, b1] (v0 / v1: the block
+// has rows) are known without classify_tile: [pf_lo, pf_hi] where both blocks
+// are FULL, [wf_lo, wf_hi] where block 0 is past its key hull (EMPTY) and
+// block 1 is FULL.  Empty ranges have lo > hi.
+struct FastRanges {
+  int32_t pf_lo, pf_hi, wf_lo, wf_hi;
+};
+
+CHIA_HD FastRanges fast_ranges(const MaskGeom& g, int32_t a0, int32_t b0, bool v0, int32_t a1, int32_t b1, bool v1,
+                               int32_t bn) {
+  FastRanges r{1, 0, 1, 0};
+  // FULL band tiles of a block: c >= key_lo(b), d <= key_hi(a), d <= S - 1
+  const int32_t ilo0 = key_lo(g, b0), ihi0 = key_hi(g, a0), ilo1 = key_lo(g, b1), ihi1 = key_hi(g, a1);
+  const bool f0 = v0 && ilo0 <= ihi0, f1 = v1 && ilo1 <= ihi1;
+  const int32_t lo0 = ceil_div(ilo0, bn), hi0 = imin32(floor_div(ihi0 + 1, bn), g.S / bn) - 1;
+  const int32_t lo1 = ceil_div(ilo1, bn), hi1 = imin32(floor_div(ihi1 + 1, bn), g.S / bn) - 1;
+  if (f0 && f1) {
+    r.pf_lo = imax32(lo0, lo1);
+    r.pf_hi = imin32(hi0, hi1);
+  }
+  if (f1) {
+    // block 0 sees no key after its hull end key_hi(b0)
+    const int32_t ulo0 = key_lo(g, a0), uhi0 = key_hi(g, b0);
+    const int32_t after0 = (v0 && ulo0 <= uhi0) ? uhi0 / bn + 1 : 0;
+    r.wf_lo = imax32(lo1, after0);
+    r.wf_hi = hi1;
+  }
+  return r;
+}
+
 // KV tiles of width bn that queries [a, b] may touch: [0, n_pre) followed by
 // [start2, start2 + n2).
 struct TileRange {

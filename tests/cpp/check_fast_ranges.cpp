@@ -1,0 +1,74 @@
+// Brute-force check of fast_ranges (chia_proj_amd/csrc/mask.h) against
+// classify_tile: every band key tile the kernel runs without classification
+// must have the class the fast path assumes.  Built and run by
+// tests/test_mask_fast_ranges.py; exits non-zero on the first mismatch.
+#include <cstdio>
+#include <initializer_list>
+
+#include "mask.h"
+
+using namespace chia;
+
+int main() {
+  const int bn = 64;
+  long checked = 0, fast = 0;
+  const int seqs[] = {1, 63, 64, 65, 200, 511, 700, 1024};
+  const int windows[] = {0, 1, 5, 64, 129, 300};
+  const int dils[] = {1, 2, 3};
+  const int blocks[] = {0, 33, 128, 256};
+  const int prefixes[] = {0, 40, 130};
+  const int bmhs[] = {64, 128};  // rows per row block (2 or 4 wavefronts)
+  for (int S : seqs)
+    for (int causal = 0; causal < 2; ++causal)
+      for (int w : windows)
+        for (int d : dils)
+          for (int blk : blocks)
+            for (int pre : prefixes) {
+              if (d > 1 && pre > 0) continue;
+              const MaskSpec m = make_mask_spec(S, causal, w, d, blk, pre);
+              for (int r = 0; r < num_residues(m); ++r) {
+                const MaskGeom g = residue_geom(m, r);
+                if (g.S <= 0) continue;
+                for (int bmh : bmhs) {
+                  const int nblk = (g.S + bmh - 1) / bmh;
+                  for (int b0 = 0; b0 < nblk; ++b0)
+                    for (int b1 : {b0, b0 + 1, nblk - 1 - b0, -1}) {
+                      if (b1 >= nblk) continue;
+                      for (int wave = 0; wave < bmh / 32; ++wave) {
+                        const int a0 = b0 * bmh + 32 * wave, a1 = (b1 >= 0 ? b1 : b0) * bmh + 32 * wave;
+                        const bool v0 = a0 < g.S, v1 = b1 >= 0 && a1 < g.S;
+                        const int e0 = imin32(a0 + 31, g.S - 1), e1 = imin32(a1 + 31, g.S - 1);
+                        const FastRanges fr = fast_ranges(g, a0, e0, v0, a1, e1, v1, bn);
+                        const int n_pre = (g.prefix + bn - 1) / bn;
+                        for (int t = n_pre; t <= g.S / bn + 1; ++t) {
+                          const int c = bn * t, dd = c + bn - 1;
+                          if (c > g.S - 1) break;
+                          const int k0 = v0 ? classify_tile(g, a0, e0, c, dd) : (int)TILE_EMPTY;
+                          const int k1 = v1 ? classify_tile(g, a1, e1, c, dd) : (int)TILE_EMPTY;
+                          ++checked;
+                          const bool in_p = t >= fr.pf_lo && t <= fr.pf_hi;
+                          const bool in_w = t >= fr.wf_lo && t <= fr.wf_hi;
+                          if (in_p && !in_w && !(k0 == TILE_FULL && k1 == TILE_FULL)) {
+                            std::printf("PAIR mismatch S=%d c=%d w=%d d=%d blk=%d p=%d r=%d bmh=%d a0=%d a1=%d t=%d k=%d,%d\n",
+                                        S, causal, w, d, blk, pre, r, bmh, a0, a1, t, k0, k1);
+                            return 1;
+                          }
+                          if (in_w && !in_p && !(k0 == TILE_EMPTY && k1 == TILE_FULL)) {
+                            std::printf("WIDE mismatch S=%d c=%d w=%d d=%d blk=%d p=%d r=%d bmh=%d a0=%d a1=%d t=%d k=%d,%d\n",
+                                        S, causal, w, d, blk, pre, r, bmh, a0, a1, t, k0, k1);
+                            return 1;
+                          }
+                          if (in_p && in_w) {
+                            std::printf("overlapping fast ranges S=%d t=%d\n", S, t);
+                            return 1;
+                          }
+                          fast += in_p || in_w;
+                        }
+                      }
+                    }
+                }
+              }
+            }
+  std::printf("checked %ld band tiles, %ld on a fast path\n", checked, fast);
+  return 0;
+}
