@@ -20,7 +20,11 @@
 //     tile t+2 is in flight while tile t is computed, one barrier per tile.
 //     Each wavefront classifies the tile against its own rows and skips it
 //     (EMPTY), runs it unmasked (FULL) or with the per-element predicate
-//     (PARTIAL).
+//     (PARTIAL); band tiles inside precomputed ranges (fast_ranges) are known
+//     to be FULL without classifying;
+//   * a tile is one step: four 32 x 32 score blocks (two query blocks x two
+//     key blocks, PAIR) or, when only block 1 sees it, two blocks of block 1
+//     (WIDE); all QK^T MFMAs of the step come before its softmax.
 //
 // Matrix-core formulation (v_mfma_f32_32x32x16_bf16, fp32 accumulate)
 //   S^T[key, query] = K Q^T : A = K rows (ds_read_b128), B = Q rows kept in
@@ -42,9 +46,9 @@
 //   the four rows x 32 bytes of one transposed-read group do.  With rows of
 //   a multiple of 128 bytes every fragment offset is a per-lane base XOR a
 //   compile-time constant.
-//   The softmax runs per 32-key block in the exp2 domain with a lazily moved
+//   The softmax runs per tile in the exp2 domain with a lazily moved
 //   reference max: the running max (and the O / l rescale) only changes when
-//   a block's max exceeds it by more than kRescaleLog2, so p <= 2^kRescaleLog2.
+//   a tile's max exceeds it by more than kRescaleLog2, so p <= 2^kRescaleLog2.
 //   The row sum l accumulates the bf16-rounded weights the PV MFMA consumes
 //   (v_dot2c_f32_bf16 against (1, 1): one instruction per two weights).
 #pragma once
