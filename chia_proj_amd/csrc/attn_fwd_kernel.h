@@ -106,13 +106,25 @@ template <bool V>
 struct BoolTag {
   static constexpr bool value = V;
 };
+template <int V>
+struct IntTag {
+  static constexpr int value = V;
+};
 
-// LDS stages of the K/V pipeline: 3 (tile t+2 in flight while t is computed)
-// for 4-wavefront workgroups, 2 for 2-wavefront ones so that four of them fit
-// in a CU's 160 KB of LDS.
+// K/V tiles whose DMA is in flight beyond the one being computed: two for
+// 4-wavefront workgroups, one for 2-wavefront ones (whose 2 LDS stages let
+// four workgroups share a CU's 160 KB of LDS).
 template <int NW>
-struct Stages {
-  static constexpr int value = NW == 2 ? 2 : 3;
+struct Ahead {
+  static constexpr int value = NW == 2 ? 1 : 2;
+};
+// The software-pipelined run (below) is compiled where its registers fit in
+// the two-waves-per-SIMD budget without spilling: head_dim 64, 4 wavefronts,
+// sigmoid / ReLU without a score modifier.  It needs one more LDS stage than
+// the plain loop (4 x 16 KB per workgroup, still two per CU).
+template <int D, int NW, int NORM, bool ALIBI, bool SOFTCAP>
+struct Pipelined {
+  static constexpr bool value = D == 64 && NW == 4 && NORM != NORM_SOFTMAX && !ALIBI && !SOFTCAP;
 };
 
 // 32-bit LDS address of a generic pointer into __shared__ memory.
@@ -194,7 +206,8 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
 
-  constexpr int NS = Stages<NW>::value;
+  constexpr bool kPipe = Pipelined<D, NW, NORM, ALIBI, SOFTCAP>::value;
+  constexpr int NS = Ahead<NW>::value + (kPipe ? 2 : 1);
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
 
   const int tid = threadIdx.x;
@@ -555,21 +568,16 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
   // ---- main loop: NS LDS stages, one barrier per tile ------------------------
   // Iteration it waits for its own DMA of tile it (leaving the loads of the
-  // next NS-2 tiles in flight), then the barrier makes every wavefront's part
-  // of tile it visible and guarantees stage (it+NS-1) % NS -- last read in
-  // iteration it-1 -- is free for the DMA of tile it+NS-1.  The barrier is a
-  // bare s_barrier: a __syncthreads() fence would also wait for the loads
-  // still in flight.
-#pragma unroll
-  for (int t = 0; t < NS - 1; ++t)
-    if (t < ntiles) issue_tile(tile_at(tr, t) * BN, t);
-  // Band tiles whose class is known without classifying (both blocks FULL,
-  // or block 0 done and block 1 FULL); everything else is classified.
-  const FastRanges fr = fast_ranges(g, row0[0], imin32(row0[0] + 31, g.S - 1), valid[0], row0[1],
-                                    imin32(row0[1] + 31, g.S - 1), valid[1], BN);
-  for (int it = 0; it < ntiles; ++it) {
-    const int jt0 = tile_at(tr, it) * BN;
-    if constexpr (NS == 3) {
+  // next AHEAD-1 tiles in flight), then the barrier makes every wavefront's
+  // part of tile it visible and frees the stage that the DMA of tile
+  // it+AHEAD overwrites: tile it+AHEAD-NS, whose last reads came before this
+  // barrier (in the pipelined run, the V tile of the pending step is read
+  // after the barrier of the next tile, hence NS = AHEAD + 2 there).  The
+  // barrier is a bare s_barrier: a __syncthreads() fence would also wait for
+  // the loads still in flight.
+  constexpr int AHEAD = Ahead<NW>::value;
+  auto sync_tile = [&](int it) __attribute__((always_inline)) {
+    if constexpr (AHEAD == 2) {
       if (it + 1 < ntiles) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
       else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else {
@@ -577,7 +585,214 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (it + NS - 1 < ntiles) issue_tile(tile_at(tr, it + NS - 1) * BN, (it + NS - 1) % NS);
+    if (it + AHEAD < ntiles) issue_tile(tile_at(tr, it + AHEAD) * BN, (it + AHEAD) % NS);
+  };
+#pragma unroll
+  for (int t = 0; t < AHEAD; ++t)
+    if (t < ntiles) issue_tile(tile_at(tr, t) * BN, t);
+  // Band tiles whose class is known without classifying (both blocks FULL,
+  // or block 0 done and block 1 FULL); everything else is classified.
+  const FastRanges fr = fast_ranges(g, row0[0], imin32(row0[0] + 31, g.S - 1), valid[0], row0[1],
+                                    imin32(row0[1] + 31, g.S - 1), valid[1], BN);
+
+  // ---- pipelined run over the tiles both blocks see in full -----------------
+  // A step is one 32-key block kb of a tile for both query blocks (two 32 x 32
+  // score blocks).  With step c pending (its scores in a register buffer),
+  // step n runs as: QK^T MFMAs of n beside the exponentials of c, then PV of c
+  // beside the score modifier and row max of n, then the (rare) rescale for
+  // n.  Steps alternate between two score buffers: kb 0 steps use buffer 0,
+  // kb 1 steps buffer 1, so the buffer of each step is known at compile time.
+  auto p_qk = [&](const char* St, int kb, f32x16_t* sa) __attribute__((always_inline)) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sa[st][e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
+      sa[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[0][kk], sa[0], 0, 0, 0);
+      sa[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[1][kk], sa[1], 0, 0, 0);
+    }
+  };
+  auto p_score = [&](int jt0, int kb, f32x16_t* sa, float* mx) __attribute__((always_inline)) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      if constexpr (!kPlainSoftmax && !kRawRelu) {
+        const int i = row0[st] + lq;
+        const int jbase = jt0 + 32 * kb + 4 * lh;
+        const float ksb = ALIBI ? ks * (float)(jbase - i) + k0 : k0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int rc = 8 * (e >> 2) + (e & 3);
+          const float qkv = sa[st][e];
+          float lin;
+          if constexpr (ALIBI) lin = __builtin_fmaf(qkv, kq, __builtin_fmaf(ks, (float)rc, ksb));
+          else if constexpr (NORM == NORM_SIGMOID && !SOFTCAP) lin = __builtin_fmaf(qkv, kq, k0);
+          else lin = qkv * kq;
+          if constexpr (SOFTCAP) {
+            const float u = __builtin_amdgcn_exp2f(lin);
+            sa[st][e] = __builtin_fmaf(__builtin_amdgcn_rcpf(1.0f + u), sc_a, sc_b);
+          } else {
+            sa[st][e] = lin;
+          }
+        }
+      }
+      if constexpr (NORM == NORM_SOFTMAX) {
+        float m = sa[st][0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) m = fmaxf(m, sa[st][e]);
+        mx[st] = m;
+      }
+    }
+  };
+  auto p_update = [&](const float* mx) __attribute__((always_inline)) {
+    if constexpr (NORM == NORM_SOFTMAX) {
+      float m_new[QB];
+      bool moved = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float m = xhalf_max(mx[qb]);
+        if constexpr (kPlainSoftmax) m = m * kq;  // kq > 0
+        m_new[qb] = (m > m_run[qb] + kRescaleLog2) ? m : m_run[qb];
+        moved |= m_new[qb] != m_run[qb];
+      }
+      if (__any(moved)) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float alpha = (m_run[qb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new[qb]);
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[db][qb][e] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) m_run[qb] = m_new[qb];
+    }
+  };
+  auto p_expo = [&](f32x16_t* sa, uint32_t (*pk)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      if constexpr (NORM == NORM_SOFTMAX) {
+        const float m_use = (m_run[st] == -INFINITY) ? 0.f : m_run[st];
+        float ls = l_run[st];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          float p0, p1;
+          if constexpr (kPlainSoftmax) {
+            p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[st][2 * w], kq, -m_use));
+            p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sa[st][2 * w + 1], kq, -m_use));
+          } else {
+            p0 = __builtin_amdgcn_exp2f(sa[st][2 * w] - m_use);
+            p1 = __builtin_amdgcn_exp2f(sa[st][2 * w + 1] - m_use);
+          }
+          const bf16x2_t pb = pack2(p0, p1);
+          ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);
+          pk[st][w] = __builtin_bit_cast(uint32_t, pb);
+        }
+        l_run[st] = ls;
+      } else {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+          float p0 = sa[st][2 * w], p1 = sa[st][2 * w + 1];
+          if constexpr (NORM == NORM_SIGMOID) {
+            p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p0));
+            p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p1));
+          } else {
+            p0 = fmaxf(p0, 0.f);
+            p1 = fmaxf(p1, 0.f);
+          }
+          pk[st][w] = __builtin_bit_cast(uint32_t, pack2(p0, p1));
+        }
+      }
+    }
+  };
+  auto p_pv = [&](const char* St, int kb, uint32_t (*pk)[8]) __attribute__((always_inline)) {
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int c = 2 * kb + half;
+      bf16x8_t pf[2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const u32x4_t w = {pk[st][4 * half], pk[st][4 * half + 1], pk[st][4 * half + 2], pk[st][4 * half + 3]};
+        pf[st] = __builtin_bit_cast(bf16x8_t, w);
+      }
+#pragma unroll
+      for (int db = 0; db < DB; db += 2) {
+        const char* va = St + 16 * c * RP + (v_lane ^ (64 * db));
+        const char* vb = St + 16 * c * RP + (v_lane ^ (64 * (db + 1)));
+        const i16x4_t lo0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)va);
+        const i16x4_t hi0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(va + 8 * RP));
+        const i16x4_t lo1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vb);
+        const i16x4_t hi1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vb + 8 * RP));
+        const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo0, hi0, 0, 1, 2, 3, 4, 5, 6, 7));
+        const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo1, hi1, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          oacc[db][st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf[st], oacc[db][st], 0, 0, 0);
+          oacc[db + 1][st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf[st], oacc[db + 1][st], 0, 0, 0);
+        }
+      }
+    }
+  };
+  // One step with step c pending in sb[P]; the new step goes to sb[1 - P].
+  auto p_body = [&](f32x16_t (*sb)[2], auto ptag, const char* Sc, int kbc, const char* Sn, int jtn, int kbn)
+      __attribute__((always_inline)) {
+    constexpr int P = decltype(ptag)::value;
+    p_qk(Sn, kbn, sb[1 - P]);
+    uint32_t pk[2][8];
+    p_expo(sb[P], pk);
+    p_pv(Sc, kbc, pk);
+    float mx[2];
+    p_score(jtn, kbn, sb[1 - P], mx);
+    p_update(mx);
+  };
+  // Iterations [ia, ib) of tiles both blocks see in full, ib > ia.
+  auto run_pipelined = [&](int ia, int ib) __attribute__((always_inline)) {
+    f32x16_t sb[2][2];
+    sync_tile(ia);
+    const char* S0 = lds + (ia % NS) * STAGE_BYTES;
+    const int j0 = tile_at(tr, ia) * BN;
+    {
+      float mx[2];
+      p_qk(S0, 0, sb[0]);
+      p_score(j0, 0, sb[0], mx);
+      p_update(mx);
+    }
+    p_body(sb, IntTag<0>{}, S0, 0, S0, j0, 1);
+    const char* Sp = S0;
+    for (int it = ia + 1; it < ib; ++it) {
+      sync_tile(it);
+      const char* St = lds + (it % NS) * STAGE_BYTES;
+      const int jt0 = tile_at(tr, it) * BN;
+      p_body(sb, IntTag<1>{}, Sp, 1, St, jt0, 0);
+      p_body(sb, IntTag<0>{}, St, 0, St, jt0, 1);
+      Sp = St;
+    }
+    uint32_t pk[2][8];
+    p_expo(sb[1], pk);
+    p_pv(Sp, 1, pk);
+  };
+  // The pipelined run covers the band tiles of [fr.pf_lo, fr.pf_hi].
+  int ia = ntiles, ib = ntiles;
+  if constexpr (kPipe) {
+    const int lo = imax32(fr.pf_lo, tr.start2), hi = imin32(fr.pf_hi, tr.start2 + tr.n2 - 1);
+    if (lo <= hi) {
+      ia = tr.n_pre + (lo - tr.start2);
+      ib = tr.n_pre + (hi - tr.start2) + 1;
+    }
+  }
+
+  for (int it = 0; it < ntiles; ++it) {
+    if (it == ia) {
+      run_pipelined(ia, ib);
+      it = ib - 1;
+      continue;
+    }
+    const int jt0 = tile_at(tr, it) * BN;
+    sync_tile(it);
     const char* St = lds + (it % NS) * STAGE_BYTES;
     int act = 0;
     bool masked[QB] = {false, false};
