@@ -124,7 +124,7 @@ struct Ahead {
 // the plain loop (4 x 16 KB per workgroup, still two per CU).
 template <int D, int NW, int NORM, bool ALIBI, bool SOFTCAP>
 struct Pipelined {
-  static constexpr bool value = D == 64 && NW == 4 && NORM != NORM_SOFTMAX && !ALIBI && !SOFTCAP;
+  static constexpr bool value = NW == 4 && NORM != NORM_SOFTMAX && !ALIBI && !SOFTCAP;
 };
 
 // 32-bit LDS address of a generic pointer into __shared__ memory.
