@@ -205,6 +205,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   static_assert(KB == 2, "a WIDE step covers the two key blocks of a tile");
   constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
+  // Softcapped softmax keeps r = 1 / (1 + 2^(2 s log2e / cap)) per score; the
+  // capped score in log2 units is t = sc_a r + sc_b (sc_a < 0), folded into
+  // the exponential's argument together with the reference max.
+  constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
 
   constexpr bool kPipe = Pipelined<D, NW, NORM, ALIBI, SOFTCAP>::value;
   constexpr int NS = Ahead<NW>::value + (kPipe ? 2 : 1);
@@ -435,7 +439,9 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
           if constexpr (ALIBI) lin = __builtin_fmaf(qk, kq, __builtin_fmaf(ks, (float)rc, ksb));
           else if constexpr (NORM == NORM_SIGMOID && !SOFTCAP) lin = __builtin_fmaf(qk, kq, k0);
           else lin = qk * kq;
-          if constexpr (SOFTCAP) {
+          if constexpr (kCapR) {
+            sacc[st][e] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(lin));
+          } else if constexpr (SOFTCAP) {
             const float u = __builtin_amdgcn_exp2f(lin);
             sacc[st][e] = __builtin_fmaf(__builtin_amdgcn_rcpf(1.0f + u), sc_a, sc_b);
           } else {
@@ -457,7 +463,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
           for (int e = 0; e < 16; ++e) {
             const int rc = 8 * (e >> 2) + (e & 3);
             const bool vis = (rc < vpre) | ((rc >= vlo) & (rc <= vhi));
-            sacc[st][e] = vis ? sacc[st][e] : ((NORM == NORM_SIGMOID) ? INFINITY : -INFINITY);
+            sacc[st][e] = vis ? sacc[st][e] : ((NORM == NORM_SIGMOID || kCapR) ? INFINITY : -INFINITY);
           }
         }
       }
@@ -471,8 +477,14 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 #pragma unroll
       for (int st = 0; st < NSTR; ++st) {
         float mx = sacc[st][0];
+        if constexpr (kCapR) {  // t = sc_a r + sc_b with sc_a < 0: max t <-> min r
 #pragma unroll
-        for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+          for (int e = 1; e < 16; ++e) mx = fminf(mx, sacc[st][e]);
+          mx = __builtin_fmaf(mx, sc_a, sc_b);
+        } else {
+#pragma unroll
+          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+        }
         mq[qb_of(st)] = fmaxf(mq[qb_of(st)], mx);
       }
       float m_new[QB];
@@ -509,6 +521,9 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
           if constexpr (kPlainSoftmax) {
             p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, -m_use));
             p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, -m_use));
+          } else if constexpr (kCapR) {
+            p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], sc_a, sc_b - m_use));
+            p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], sc_a, sc_b - m_use));
           } else {
             p0 = __builtin_amdgcn_exp2f(sacc[st][2 * w] - m_use);
             p1 = __builtin_amdgcn_exp2f(sacc[st][2 * w + 1] - m_use);
@@ -786,10 +801,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   }
 
   for (int it = 0; it < ntiles; ++it) {
-    if (it == ia) {
-      run_pipelined(ia, ib);
-      it = ib - 1;
-      continue;
+    if constexpr (kPipe) {
+      if (it == ia) {
+        run_pipelined(ia, ib);
+        it = ib - 1;
+        continue;
+      }
     }
     const int jt0 = tile_at(tr, it) * BN;
     sync_tile(it);
