@@ -16,15 +16,18 @@
 //     the pair is (2i, 2i+1);
 //   * the KV loop walks only the key tiles (BN = 64 keys) the mask can reach
 //     (prefix tiles + the band hull).  K and V tiles go from HBM straight into
-//     LDS with global_load_lds_dwordx4 (no VGPR staging), three stages deep:
-//     tile t+2 is in flight while tile t is computed, one barrier per tile.
+//     LDS with global_load_lds_dwordx4 (no VGPR staging) into four stages
+//     (two for 2-wavefront workgroups), up to three tiles ahead of the one
+//     computed, one barrier per step.
 //     Each wavefront classifies the tile against its own rows and skips it
 //     (EMPTY), runs it unmasked (FULL) or with the per-element predicate
 //     (PARTIAL); band tiles inside precomputed ranges (fast_ranges) are known
 //     to be FULL without classifying;
 //   * a tile is one step: four 32 x 32 score blocks (two query blocks x two
 //     key blocks, PAIR) or, when only block 1 sees it, two blocks of block 1
-//     (WIDE); all QK^T MFMAs of the step come before its softmax.
+//     (WIDE); two consecutive tiles that only block 1 sees, in every
+//     wavefront, make one four-block step (WIDE2).  All QK^T MFMAs of a step
+//     come before its softmax.
 //
 // Matrix-core formulation (v_mfma_f32_32x32x16_bf16, fp32 accumulate)
 //   S^T[key, query] = K Q^T : A = K rows (ds_read_b128), B = Q rows kept in
@@ -111,17 +114,8 @@ struct IntTag {
   static constexpr int value = V;
 };
 
-// K/V tiles whose DMA is in flight beyond the one being computed: two for
-// 4-wavefront workgroups, one for 2-wavefront ones (whose 2 LDS stages let
-// four workgroups share a CU's 160 KB of LDS).
-template <int NW>
-struct Ahead {
-  static constexpr int value = NW == 2 ? 1 : 2;
-};
-// The software-pipelined run (below) is compiled where its registers fit in
-// the two-waves-per-SIMD budget without spilling: head_dim 64, 4 wavefronts,
-// sigmoid / ReLU without a score modifier.  It needs one more LDS stage than
-// the plain loop (4 x 16 KB per workgroup, still two per CU).
+// The software-pipelined run (below) is compiled where its registers fit
+// without spilling: 4 wavefronts, sigmoid / ReLU without a score modifier.
 template <int D, int NW, int NORM, bool ALIBI, bool SOFTCAP>
 struct Pipelined {
   static constexpr bool value = NW == 4 && NORM != NORM_SOFTMAX && !ALIBI && !SOFTCAP;
@@ -211,7 +205,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
 
   constexpr bool kPipe = Pipelined<D, NW, NORM, ALIBI, SOFTCAP>::value;
-  constexpr int NS = Ahead<NW>::value + (kPipe ? 2 : 1);
+  // LDS stages: 4 for 4-wavefront workgroups (up to three tiles in flight;
+  // WIDE2 steps hold two), 2 for 2-wavefront ones.
+  constexpr int NS = NW == 4 ? 4 : 2;
+  constexpr bool kWide2 = NW == 4 && !kPipe;  // (the pipelined kernels keep their registers for the run)
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
 
   const int tid = threadIdx.x;
@@ -400,11 +397,17 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // per tile, so the only branch between the first MFMA and the last one is
   // the (rare) rescale.  masked[qb] selects the per-element predicate for a
   // block the tile only partly covers.
-  auto tile_step = [&](const char* St, int jt0, const bool* masked, auto wide_tag) {
-    constexpr bool WIDE = decltype(wide_tag)::value;
-    constexpr int NSTR = WIDE ? 2 : 4;
+  //   WIDE2: four streams, query block 1 x the four key blocks of two
+  //     consecutive tiles (St, St2) -- two WIDE tiles behind one barrier.
+  auto tile_step = [&](const char* St, const char* St2, int jt0, const bool* masked, auto mode_tag) {
+    constexpr int MODE = decltype(mode_tag)::value;  // 0 PAIR, 1 WIDE, 2 WIDE2
+    constexpr bool WIDE = MODE != 0;
+    constexpr int NSTR = MODE == 1 ? 2 : 4;
+    constexpr int NKB = MODE == 2 ? 2 * KB : KB;  // key blocks of the step
     auto qb_of = [](int st) { return WIDE ? 1 : (st & 1); };
     auto kb_of = [](int st) { return WIDE ? st : (st >> 1); };
+    // key block kb (0 .. NKB-1) of the step: its stage and first row there
+    auto kb_base = [&](int kb) { return (kb < KB ? St : St2) + 32 * (kb % KB) * RP; };
     f32x16_t sacc[NSTR];
 #pragma unroll
     for (int st = 0; st < NSTR; ++st)
@@ -413,10 +416,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
     // S^T = K Q^T, key block by key block
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
+    for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
       for (int kk = 0; kk < DK; ++kk) {
-        const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
+        const bf16x8_t a = *(const bf16x8_t*)(kb_base(kb) + (k_lane ^ (32 * kk)));
 #pragma unroll
         for (int st = 0; st < NSTR; ++st)
           if (kb_of(st) == kb)
@@ -556,12 +559,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     typedef short i16x8_t __attribute__((ext_vector_type(8)));
     static_assert(DB % 2 == 0, "d-blocks are read in pairs");
 #pragma unroll
-    for (int c = 0; c < 2 * KB; ++c) {
+    for (int c = 0; c < 2 * NKB; ++c) {
       const int kb = c >> 1, half = c & 1;
 #pragma unroll
       for (int db = 0; db < DB; db += 2) {
-        const char* va = St + 16 * c * RP + (v_lane ^ (64 * db));
-        const char* vb = St + 16 * c * RP + (v_lane ^ (64 * (db + 1)));
+        const char* va = kb_base(kb) + 16 * half * RP + (v_lane ^ (64 * db));
+        const char* vb = kb_base(kb) + 16 * half * RP + (v_lane ^ (64 * (db + 1)));
         const i16x4_t lo0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)va);
         const i16x4_t hi0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(va + 8 * RP));
         const i16x4_t lo1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)vb);
@@ -581,34 +584,60 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     }
   };
 
-  // ---- main loop: NS LDS stages, one barrier per tile ------------------------
-  // Iteration it waits for its own DMA of tile it (leaving the loads of the
-  // next AHEAD-1 tiles in flight), then the barrier makes every wavefront's
-  // part of tile it visible and frees the stage that the DMA of tile
-  // it+AHEAD overwrites: tile it+AHEAD-NS, whose last reads came before this
-  // barrier (in the pipelined run, the V tile of the pending step is read
-  // after the barrier of the next tile, hence NS = AHEAD + 2 there).  The
-  // barrier is a bare s_barrier: a __syncthreads() fence would also wait for
-  // the loads still in flight.
-  constexpr int AHEAD = Ahead<NW>::value;
-  auto sync_tile = [&](int it) __attribute__((always_inline)) {
-    if constexpr (AHEAD == 2) {
-      if (it + 1 < ntiles) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
+  // ---- main loop: NS LDS stages, one barrier per step ------------------------
+  // Tiles [0, dma_next) have been issued; tile T goes to stage T % NS.  A
+  // step over tiles [it, it + n) waits until those have landed (the loads of
+  // later tiles stay in flight), then the barrier makes every wavefront's
+  // part of them visible, and the DMA continues up to tile oldest + NS - 1,
+  // where `oldest` is the first tile still read after this barrier: the tile
+  // it overwrites, oldest - 1, was last read before it.  (oldest = it, or
+  // it - 1 in kernels with a pipelined run, which reads the pending step's V
+  // tile after the next tile's barrier.)  Every wavefront loads part of every
+  // tile, so the steps, barriers and DMA issues must be the same in all
+  // wavefronts of the workgroup: only workgroup-uniform values decide them
+  // (the tile range, the WIDE2 range below, and `oldest` fixed per kernel,
+  // since the other wavefronts may still be inside their pipelined run).
+  // The barrier is a bare s_barrier: a __syncthreads() fence would also wait
+  // for the loads still in flight.
+  // A step frees as many stages as it had tiles, so a sync issues at most
+  // kIssue tiles (the previous step's count), and at most kFly tiles beyond
+  // the step's own are in flight when it waits: NS - 2, or NS - 3 where the
+  // pipelined run keeps one more stage.  Waiting for fewer tiles in flight
+  // than there are is always safe, so the vmcnt cases stop at kFly.
+  constexpr int kIssue = kWide2 ? 2 : 1;
+  constexpr int kFly = NS - (kPipe ? 3 : 2);
+  static_assert(kFly >= 0 && kFly <= 2, "vmcnt cases cover up to two tiles in flight");
+  int dma_next = 0;
+  auto issue_upto = [&](int last) __attribute__((always_inline)) {
+    last = imin32(last, ntiles - 1);
+#pragma unroll
+    for (int k = 0; k < kIssue; ++k)
+      if (dma_next <= last) {
+        issue_tile(tile_at(tr, dma_next) * BN, dma_next % NS);
+        ++dma_next;
+      }
+  };
+  auto sync_step = [&](int it, int n, int oldest) __attribute__((always_inline)) {
+    const int inflight = dma_next - (it + n);  // tiles allowed to stay in flight
+    if (kFly >= 2 && inflight >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NDMA) : "memory");
+    else if (kFly >= 1 && inflight >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (it + AHEAD < ntiles) issue_tile(tile_at(tr, it + AHEAD) * BN, (it + AHEAD) % NS);
+    issue_upto(oldest + NS - 1);
   };
-#pragma unroll
-  for (int t = 0; t < AHEAD; ++t)
-    if (t < ntiles) issue_tile(tile_at(tr, t) * BN, t);
+  auto sync_tile = [&](int it) __attribute__((always_inline)) { sync_step(it, 1, kPipe ? it - 1 : it); };
+  // prologue: the first kFly + 1 tiles (the first sync issues the next one)
+  for (int t = 0; t <= kFly && t < ntiles; ++t) issue_tile(tile_at(tr, t) * BN, t);
+  dma_next = imin32(kFly + 1, ntiles);
   // Band tiles whose class is known without classifying (both blocks FULL,
   // or block 0 done and block 1 FULL); everything else is classified.
   const FastRanges fr = fast_ranges(g, row0[0], imin32(row0[0] + 31, g.S - 1), valid[0], row0[1],
                                     imin32(row0[1] + 31, g.S - 1), valid[1], BN);
+  // WIDE2 tiles: block 0 done and block 1 FULL in every wavefront, since a
+  // WIDE2 step changes the barrier count.
+  TileSpan w2{1, 0};
+  if constexpr (kWide2) w2 = wide_range_all(g, blk0 * BMH, (blk1 >= 0 ? blk1 : blk0) * BMH, blk1 >= 0, NW, BN);
 
   // ---- pipelined run over the tiles both blocks see in full -----------------
   // A step is one 32-key block kb of a tile for both query blocks (two 32 x 32
@@ -809,6 +838,18 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       }
     }
     const int jt0 = tile_at(tr, it) * BN;
+    // Two consecutive tiles that only block 1 sees, both in full: one WIDE2
+    // step behind one barrier.
+    if constexpr (kWide2) {
+      const int t = jt0 / BN;
+      if (it >= tr.n_pre && it + 1 < ntiles && t >= w2.lo && t + 1 <= w2.hi) {
+        sync_step(it, 2, it);
+        const bool none[QB] = {false, false};
+        tile_step(lds + (it % NS) * STAGE_BYTES, lds + ((it + 1) % NS) * STAGE_BYTES, jt0, none, IntTag<2>{});
+        ++it;
+        continue;
+      }
+    }
     sync_tile(it);
     const char* St = lds + (it % NS) * STAGE_BYTES;
     int act = 0;
@@ -830,10 +871,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     // case of a zigzag pair past the light block's diagonal).  A tile that
     // only block 0 sees runs the PAIR path with block 1 fully masked.
     if (act == 2) {
-      tile_step(St, jt0, masked, BoolTag<true>{});
+      tile_step(St, St, jt0, masked, IntTag<1>{});
     } else if (act != 0) {
       masked[1] = masked[1] || act == 1;
-      tile_step(St, jt0, masked, BoolTag<false>{});
+      tile_step(St, St, jt0, masked, IntTag<0>{});
     }
   }
 

@@ -120,6 +120,26 @@ CHIA_HD FastRanges fast_ranges(const MaskGeom& g, int32_t a0, int32_t b0, bool v
   return r;
 }
 
+// Band tiles in the WIDE range of every wavefront of a workgroup: wavefront w
+// holds query blocks [r0 + 32 w, +32) and, when has1, [r1 + 32 w, +32).  A
+// step that decides the workgroup's barrier schedule may only use this
+// intersection, not one wavefront's own range.  Empty when lo > hi.
+struct TileSpan {
+  int32_t lo, hi;
+};
+
+CHIA_HD TileSpan wide_range_all(const MaskGeom& g, int32_t r0, int32_t r1, bool has1, int32_t nw, int32_t bn) {
+  TileSpan s{0, 0x7fffffff};
+  for (int32_t w = 0; w < nw; ++w) {
+    const int32_t a0 = r0 + 32 * w, a1 = r1 + 32 * w;
+    const FastRanges f = fast_ranges(g, a0, imin32(a0 + 31, g.S - 1), a0 < g.S, a1, imin32(a1 + 31, g.S - 1),
+                                     has1 && a1 < g.S, bn);
+    s.lo = imax32(s.lo, f.wf_lo);
+    s.hi = imin32(s.hi, f.wf_hi);
+  }
+  return s;
+}
+
 // KV tiles of width bn that queries [a, b] may touch: [0, n_pre) followed by
 // [start2, start2 + n2).
 struct TileRange {

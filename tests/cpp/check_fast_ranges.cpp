@@ -1,6 +1,7 @@
-// Brute-force check of fast_ranges (chia_proj_amd/csrc/mask.h) against
-// classify_tile: every band key tile the kernel runs without classification
-// must have the class the fast path assumes.  Built and run by
+// Brute-force check of fast_ranges and wide_range_all (chia_proj_amd/csrc/mask.h)
+// against classify_tile: every band key tile the kernel runs without
+// classification must have the class the fast path assumes, in every
+// wavefront for the workgroup-uniform WIDE span.  Built and run by
 // tests/test_mask_fast_ranges.py; exits non-zero on the first mismatch.
 #include <cstdio>
 #include <initializer_list>
@@ -11,7 +12,7 @@ using namespace chia;
 
 int main() {
   const int bn = 64;
-  long checked = 0, fast = 0;
+  long checked = 0, fast = 0, wide_all = 0;
   const int seqs[] = {1, 63, 64, 65, 200, 511, 700, 1024};
   const int windows[] = {0, 1, 5, 64, 129, 300};
   const int dils[] = {1, 2, 3};
@@ -34,6 +35,29 @@ int main() {
                   for (int b0 = 0; b0 < nblk; ++b0)
                     for (int b1 : {b0, b0 + 1, nblk - 1 - b0, -1}) {
                       if (b1 >= nblk) continue;
+                      // the workgroup-uniform WIDE span: WIDE in every wavefront
+                      const TileSpan all = wide_range_all(g, b0 * bmh, (b1 >= 0 ? b1 : b0) * bmh, b1 >= 0, bmh / 32, bn);
+                      const int n_pre_all = (g.prefix + bn - 1) / bn;
+                      for (int t = imax32(all.lo, n_pre_all); t <= all.hi; ++t) {
+                        const int c = bn * t, dd = c + bn - 1;
+                        if (dd > g.S - 1) {
+                          std::printf("WIDE span past the end S=%d t=%d\n", S, t);
+                          return 1;
+                        }
+                        for (int wave = 0; wave < bmh / 32; ++wave) {
+                          const int a0 = b0 * bmh + 32 * wave, a1 = (b1 >= 0 ? b1 : b0) * bmh + 32 * wave;
+                          const int k0 = a0 < g.S ? classify_tile(g, a0, imin32(a0 + 31, g.S - 1), c, dd) : (int)TILE_EMPTY;
+                          const int k1 = b1 >= 0 && a1 < g.S ? classify_tile(g, a1, imin32(a1 + 31, g.S - 1), c, dd)
+                                                             : (int)TILE_EMPTY;
+                          ++checked;
+                          if (!(k0 == TILE_EMPTY && k1 == TILE_FULL)) {
+                            std::printf("WIDE span mismatch S=%d c=%d w=%d d=%d blk=%d p=%d r=%d bmh=%d wave=%d t=%d k=%d,%d\n",
+                                        S, causal, w, d, blk, pre, r, bmh, wave, t, k0, k1);
+                            return 1;
+                          }
+                        }
+                        ++wide_all;
+                      }
                       for (int wave = 0; wave < bmh / 32; ++wave) {
                         const int a0 = b0 * bmh + 32 * wave, a1 = (b1 >= 0 ? b1 : b0) * bmh + 32 * wave;
                         const bool v0 = a0 < g.S, v1 = b1 >= 0 && a1 < g.S;
@@ -69,6 +93,6 @@ int main() {
                 }
               }
             }
-  std::printf("checked %ld band tiles, %ld on a fast path\n", checked, fast);
+  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span\n", checked, fast, wide_all);
   return 0;
 }
