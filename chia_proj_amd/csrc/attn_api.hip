@@ -156,8 +156,13 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
   p.bias = a->bias;
   p.post_scale = a->post_scale;
 
-  const bool alibi = a->alibi_slopes != nullptr;
+  bool alibi = a->alibi_slopes != nullptr;
   const bool softcap = a->softcap > 0.f;
+  // The plain sigmoid kernel takes the bias as the factor 2^(-bias log2 e),
+  // which must be a normal float; a larger |bias| runs the general score path
+  // (the ALiBi kernel with null slopes, i.e. zero).
+  if (a->norm == CHIA_ATTN_NORM_SIGMOID && !alibi && !softcap && !(std::fabs(-a->bias * kLog2e) <= 120.f))
+    alibi = true;
   KernelFn fn = a->head_dim == 64 ? select_kernel_d64(waves, (int)a->norm, alibi, softcap)
                                   : select_kernel_d128(waves, (int)a->norm, alibi, softcap);
   void* kargs[] = {&p};

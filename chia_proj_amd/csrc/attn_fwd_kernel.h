@@ -180,6 +180,15 @@ __device__ __forceinline__ bf16x2_t pack2(float a, float b) {
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) { return __builtin_bit_cast(uint32_t, pack2(a, b)); }
 
+// max(x, 0) as one v_max_i32 on the bit pattern: negative floats and -0 are
+// negative integers, non-negative floats keep their order as integers.
+// (fmaxf of an MFMA result costs a second v_max that first quiets a possible
+// signalling NaN; here a NaN of positive sign propagates, as torch.relu does.)
+__device__ __forceinline__ float relu0(float x) {
+  const int i = __builtin_bit_cast(int, x);
+  return __builtin_bit_cast(float, i > 0 ? i : 0);
+}
+
 template <int D, int NW, int NORM, bool ALIBI, bool SOFTCAP>
 __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(const FwdParams p) {
   constexpr int BN = kBN;
@@ -203,6 +212,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // capped score in log2 units is t = sc_a r + sc_b (sc_a < 0), folded into
   // the exponential's argument together with the reference max.
   constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
+  constexpr bool kSigFold = NORM == NORM_SIGMOID && !ALIBI && !SOFTCAP;
 
   constexpr bool kPipe = Pipelined<D, NW, NORM, ALIBI, SOFTCAP>::value;
   // LDS stages: 4 for 4-wavefront workgroups (up to three tiles in flight;
@@ -247,7 +257,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
   // ---- per-head score constants --------------------------------------------
   const float hs = p.head_scale ? p.head_scale[h] : 1.0f;
-  const float slope = ALIBI ? p.alibi_slopes[h] : 0.0f;
+  const float slope = ALIBI && p.alibi_slopes ? p.alibi_slopes[h] : 0.0f;  // null: zero slopes
   const float c1 = p.scale * hs;
   const float sl = slope * (float)dil;  // bias per sub-sequence step
   float kq, ks, k0 = 0.f, sc_a = 0.f, sc_b = 0.f;
@@ -277,6 +287,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     ks = sl;
   }
   const float post = kRawRelu ? p.post_scale * c1 : p.post_scale;
+  // Plain sigmoid: Q is pre-scaled by kq (one bf16 rounding per element, at
+  // load), so a score is already the exponent, and the bias enters as the
+  // factor 2^k0: p = 1 / (1 + 2^k0 2^s).  The host routes a bias whose 2^k0
+  // is not a normal float to the general path (ALIBI with null slopes).
+  const float sig_c =
+      kSigFold ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__builtin_amdgcn_exp2f(k0)))) : 0.f;
 
   // ---- wavefront rows, Q fragments, per-row key intervals -------------------
   int row0[QB];      // first row of this wavefront's 32-row query block qb
@@ -296,6 +312,11 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     for (int kk = 0; kk < DK; ++kk) {
       u32x4_t val = *(const u32x4_t*)(src + 16 * kk);
       if (!ok) val = u32x4_t{0u, 0u, 0u, 0u};
+      if constexpr (kSigFold) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          val[w] = pack_bf16x2(__uint_as_float(val[w] << 16) * kq, __uint_as_float(val[w] & 0xffff0000u) * kq);
+      }
       qf[qb][kk] = __builtin_bit_cast(bf16x8_t, val);
     }
   }
@@ -428,7 +449,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     }
 
     // score modifier -> t (in place)
-    if constexpr (!kPlainSoftmax && !kRawRelu) {
+    if constexpr (!kPlainSoftmax && !kRawRelu && !kSigFold) {
 #pragma unroll
       for (int st = 0; st < NSTR; ++st) {
         const int i = row0[qb_of(st)] + lq;
@@ -543,12 +564,15 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
           float p0 = sacc[st][2 * w], p1 = sacc[st][2 * w + 1];
-          if constexpr (NORM == NORM_SIGMOID) {
+          if constexpr (kSigFold) {
+            p0 = __builtin_amdgcn_rcpf(__builtin_fmaf(sig_c, __builtin_amdgcn_exp2f(p0), 1.0f));
+            p1 = __builtin_amdgcn_rcpf(__builtin_fmaf(sig_c, __builtin_amdgcn_exp2f(p1), 1.0f));
+          } else if constexpr (NORM == NORM_SIGMOID) {
             p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p0));
             p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p1));
           } else {
-            p0 = fmaxf(p0, 0.f);
-            p1 = fmaxf(p1, 0.f);
+            p0 = relu0(p0);
+            p1 = relu0(p1);
           }
           pk[st][w] = __builtin_bit_cast(uint32_t, pack2(p0, p1));
         }
@@ -661,7 +685,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   auto p_score = [&](int jt0, int kb, f32x16_t* sa, float* mx) __attribute__((always_inline)) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      if constexpr (!kPlainSoftmax && !kRawRelu) {
+      if constexpr (!kPlainSoftmax && !kRawRelu && !kSigFold) {
         const int i = row0[st] + lq;
         const int jbase = jt0 + 32 * kb + 4 * lh;
         const float ksb = ALIBI ? ks * (float)(jbase - i) + k0 : k0;
@@ -740,12 +764,15 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
           float p0 = sa[st][2 * w], p1 = sa[st][2 * w + 1];
-          if constexpr (NORM == NORM_SIGMOID) {
+          if constexpr (kSigFold) {
+            p0 = __builtin_amdgcn_rcpf(__builtin_fmaf(sig_c, __builtin_amdgcn_exp2f(p0), 1.0f));
+            p1 = __builtin_amdgcn_rcpf(__builtin_fmaf(sig_c, __builtin_amdgcn_exp2f(p1), 1.0f));
+          } else if constexpr (NORM == NORM_SIGMOID) {
             p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p0));
             p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p1));
           } else {
-            p0 = fmaxf(p0, 0.f);
-            p1 = fmaxf(p1, 0.f);
+            p0 = relu0(p0);
+            p1 = relu0(p1);
           }
           pk[st][w] = __builtin_bit_cast(uint32_t, pack2(p0, p1));
         }

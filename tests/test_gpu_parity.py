@@ -119,6 +119,11 @@ EDGE = [
     ("S384_relu_softcap", 384, 64, dict(norm="relu", causal=True, softcap=5.0, post_scale=0.1)),
     ("S384_headscale", 384, 64, dict(causal=True, head_scale=[0.5, 2.0])),
     ("S384_noncausal_block_band", 384, 64, dict(causal=False, block=32, window=3)),
+    # plain sigmoid takes the bias as the factor 2^(-bias log2 e): near the end of
+    # that range (|bias log2 e| = 115), and past it (137: the general score path)
+    ("S640_sigmoid_bias_fold_limit", 640, 64, dict(norm="sigmoid", causal=False, scale=10.0, bias=-80.0)),
+    ("S640_sigmoid_bias_general", 640, 64, dict(norm="sigmoid", causal=True, scale=12.0, bias=-95.0)),
+    ("S640_sigmoid_bias_general_pos", 640, 128, dict(norm="sigmoid", causal=False, scale=12.0, bias=95.0)),
 ]
 
 
