@@ -151,6 +151,9 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
   const int waves = geo.waves;
   if (geo.workgroups >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
   p.n_wg = (int32_t)geo.workgroups;
+  p.div_pairs = make_udiv(p.n_pairs);
+  p.div_res = make_udiv(p.residues);
+  p.div_h = make_udiv(p.H);
   p.scale = a->scale;
   p.softcap = a->softcap;
   p.bias = a->bias;

@@ -92,6 +92,7 @@ struct FwdParams {
   int32_t n_pairs;            // row-block pairs per (b, h, residue 0)
   int32_t zigzag;             // pair blocks (i, n-1-i) instead of (2i, 2i+1)
   int32_t n_wg;
+  UDiv div_pairs, div_res, div_h;  // dividers by n_pairs, residues, H
   float scale, softcap, bias, post_scale;
 };
 
@@ -218,6 +219,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // LDS stages: 4 for 4-wavefront workgroups (up to three tiles in flight;
   // WIDE2 steps hold two), 2 for 2-wavefront ones.
   constexpr int NS = NW == 4 ? 4 : 2;
+  static_assert((NS & (NS - 1)) == 0, "stage index is a mask");
   constexpr bool kWide2 = NW == 4 && !kPipe;  // (the pipelined kernels keep their registers for the run)
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
 
@@ -228,11 +230,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
   // ---- workgroup -> (batch, head, residue, row-block pair) -----------------
   const int L = xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = L / p.n_pairs;
-  const int pr = L % p.n_pairs;
-  const int r = bhr % p.residues;
-  const int bh = bhr / p.residues;
-  const int h = bh % p.H, b = bh / p.H;
+  const int bhr = udiv(L, p.div_pairs);
+  const int pr = L - bhr * p.n_pairs;
+  const int bh = udiv(bhr, p.div_res);
+  const int r = bhr - bh * p.residues;
+  const int b = udiv(bh, p.div_h);
+  const int h = bh - b * p.H;
   const MaskGeom g = residue_geom(p.mask, r);
   const int nblk = (g.S + BMH - 1) / BMH;  // row blocks of this residue
   int blk0, blk1;
@@ -363,6 +366,54 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     }
   };
 
+  // ---- DMA schedule: NS LDS stages, one barrier per step --------------------
+  // Tiles [0, dma_next) have been issued; tile T goes to stage T % NS.  A
+  // step over tiles [it, it + n) waits until those have landed (the loads of
+  // later tiles stay in flight), then the barrier makes every wavefront's
+  // part of them visible, and the DMA continues up to tile oldest + NS - 1,
+  // where `oldest` is the first tile still read after this barrier: the tile
+  // it overwrites, oldest - 1, was last read before it.  (oldest = it, or
+  // it - 1 in kernels with a pipelined run, which reads the pending step's V
+  // tile after the next tile's barrier.)  Every wavefront loads part of every
+  // tile, so the steps, barriers and DMA issues must be the same in all
+  // wavefronts of the workgroup: only workgroup-uniform values decide them
+  // (the tile range, the WIDE2 range below, and `oldest` fixed per kernel,
+  // since the other wavefronts may still be inside their pipelined run).
+  // The barrier is a bare s_barrier: a __syncthreads() fence would also wait
+  // for the loads still in flight.
+  // A step frees as many stages as it had tiles, so a sync issues at most
+  // kIssue tiles (the previous step's count), and at most kFly tiles beyond
+  // the step's own are in flight when it waits: NS - 2, or NS - 3 where the
+  // pipelined run keeps one more stage.  Waiting for fewer tiles in flight
+  // than there are is always safe, so the vmcnt cases stop at kFly.
+  constexpr int kIssue = kWide2 ? 2 : 1;
+  constexpr int kFly = NS - (kPipe ? 3 : 2);
+  static_assert(kFly >= 0 && kFly <= 2, "vmcnt cases cover up to two tiles in flight");
+  int dma_next = 0;
+  auto issue_upto = [&](int last) __attribute__((always_inline)) {
+    last = imin32(last, ntiles - 1);
+#pragma unroll
+    for (int k = 0; k < kIssue; ++k)
+      if (dma_next <= last) {
+        issue_tile(tile_at(tr, dma_next) * BN, dma_next & (NS - 1));
+        ++dma_next;
+      }
+  };
+  auto sync_step = [&](int it, int n, int oldest) __attribute__((always_inline)) {
+    const int inflight = dma_next - (it + n);  // tiles allowed to stay in flight
+    if (kFly >= 2 && inflight >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NDMA) : "memory");
+    else if (kFly >= 1 && inflight >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue_upto(oldest + NS - 1);
+  };
+  auto sync_tile = [&](int it) __attribute__((always_inline)) { sync_step(it, 1, kPipe ? it - 1 : it); };
+  // prologue: the first kFly + 1 tiles (the first sync issues the next one),
+  // issued before the per-block set-up below so the loads overlap it
+  for (int t = 0; t <= kFly && t < ntiles; ++t) issue_tile(tile_at(tr, t) * BN, t);
+  dma_next = imin32(kFly + 1, ntiles);
+
   // Tile classes: each query block's key hull [ulo, uhi] and common interval
   // [ilo, ihi] (classify_tile with the row-dependent parts hoisted).
   int c_ulo[QB], c_uhi[QB], c_ilo[QB], c_ihi[QB];
@@ -482,12 +533,18 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
           // the row's key interval is recomputed here rather than kept live
           const int i = row0[qb_of(st)] + lq;
           const int jbase = jt0 + 32 * kb_of(st) + 4 * lh;
-          const int vlo = key_lo(g, i) - jbase, vhi = key_hi(g, i) - jbase, vpre = g.prefix - jbase;
+          const uint32_t hidden = hidden_bits(g, i, jbase);  // bit k: key jbase + k hidden from row i
+          // the +-inf pattern in an SGPR (loaded opaquely, so the blend below
+          // stays one three-input bitwise op instead of xor + op with a literal)
+          uint32_t hide_bits;
+          asm("s_mov_b32 %0, %1" : "=s"(hide_bits) : "i"((NORM == NORM_SIGMOID || kCapR) ? 0x7f800000 : 0xff800000));
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const int rc = 8 * (e >> 2) + (e & 3);
-            const bool vis = (rc < vpre) | ((rc >= vlo) & (rc <= vhi));
-            sacc[st][e] = vis ? sacc[st][e] : ((NORM == NORM_SIGMOID || kCapR) ? INFINITY : -INFINITY);
+            // all ones where hidden (v_bfe_i32), then a bitwise blend of the +-inf pattern
+            uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)hidden, rc, 1);
+            asm("" : "+v"(m));  // keeps the blend bitwise instead of compare + select
+            sacc[st][e] = __uint_as_float((m & hide_bits) | (~m & __float_as_uint(sacc[st][e])));
           }
         }
       }
@@ -608,52 +665,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     }
   };
 
-  // ---- main loop: NS LDS stages, one barrier per step ------------------------
-  // Tiles [0, dma_next) have been issued; tile T goes to stage T % NS.  A
-  // step over tiles [it, it + n) waits until those have landed (the loads of
-  // later tiles stay in flight), then the barrier makes every wavefront's
-  // part of them visible, and the DMA continues up to tile oldest + NS - 1,
-  // where `oldest` is the first tile still read after this barrier: the tile
-  // it overwrites, oldest - 1, was last read before it.  (oldest = it, or
-  // it - 1 in kernels with a pipelined run, which reads the pending step's V
-  // tile after the next tile's barrier.)  Every wavefront loads part of every
-  // tile, so the steps, barriers and DMA issues must be the same in all
-  // wavefronts of the workgroup: only workgroup-uniform values decide them
-  // (the tile range, the WIDE2 range below, and `oldest` fixed per kernel,
-  // since the other wavefronts may still be inside their pipelined run).
-  // The barrier is a bare s_barrier: a __syncthreads() fence would also wait
-  // for the loads still in flight.
-  // A step frees as many stages as it had tiles, so a sync issues at most
-  // kIssue tiles (the previous step's count), and at most kFly tiles beyond
-  // the step's own are in flight when it waits: NS - 2, or NS - 3 where the
-  // pipelined run keeps one more stage.  Waiting for fewer tiles in flight
-  // than there are is always safe, so the vmcnt cases stop at kFly.
-  constexpr int kIssue = kWide2 ? 2 : 1;
-  constexpr int kFly = NS - (kPipe ? 3 : 2);
-  static_assert(kFly >= 0 && kFly <= 2, "vmcnt cases cover up to two tiles in flight");
-  int dma_next = 0;
-  auto issue_upto = [&](int last) __attribute__((always_inline)) {
-    last = imin32(last, ntiles - 1);
-#pragma unroll
-    for (int k = 0; k < kIssue; ++k)
-      if (dma_next <= last) {
-        issue_tile(tile_at(tr, dma_next) * BN, dma_next % NS);
-        ++dma_next;
-      }
-  };
-  auto sync_step = [&](int it, int n, int oldest) __attribute__((always_inline)) {
-    const int inflight = dma_next - (it + n);  // tiles allowed to stay in flight
-    if (kFly >= 2 && inflight >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NDMA) : "memory");
-    else if (kFly >= 1 && inflight >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue_upto(oldest + NS - 1);
-  };
-  auto sync_tile = [&](int it) __attribute__((always_inline)) { sync_step(it, 1, kPipe ? it - 1 : it); };
-  // prologue: the first kFly + 1 tiles (the first sync issues the next one)
-  for (int t = 0; t <= kFly && t < ntiles; ++t) issue_tile(tile_at(tr, t) * BN, t);
-  dma_next = imin32(kFly + 1, ntiles);
+  // ---- main loop -------------------------------------------------------------
   // Band tiles whose class is known without classifying (both blocks FULL,
   // or block 0 done and block 1 FULL); everything else is classified.
   const FastRanges fr = fast_ranges(g, row0[0], imin32(row0[0] + 31, g.S - 1), valid[0], row0[1],
@@ -824,7 +836,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   auto run_pipelined = [&](int ia, int ib) __attribute__((always_inline)) {
     f32x16_t sb[2][2];
     sync_tile(ia);
-    const char* S0 = lds + (ia % NS) * STAGE_BYTES;
+    const char* S0 = lds + (ia & (NS - 1)) * STAGE_BYTES;
     const int j0 = tile_at(tr, ia) * BN;
     {
       float mx[2];
@@ -836,7 +848,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     const char* Sp = S0;
     for (int it = ia + 1; it < ib; ++it) {
       sync_tile(it);
-      const char* St = lds + (it % NS) * STAGE_BYTES;
+      const char* St = lds + (it & (NS - 1)) * STAGE_BYTES;
       const int jt0 = tile_at(tr, it) * BN;
       p_body(sb, IntTag<1>{}, Sp, 1, St, jt0, 0);
       p_body(sb, IntTag<0>{}, St, 0, St, jt0, 1);
@@ -872,13 +884,13 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       if (it >= tr.n_pre && it + 1 < ntiles && t >= w2.lo && t + 1 <= w2.hi) {
         sync_step(it, 2, it);
         const bool none[QB] = {false, false};
-        tile_step(lds + (it % NS) * STAGE_BYTES, lds + ((it + 1) % NS) * STAGE_BYTES, jt0, none, IntTag<2>{});
+        tile_step(lds + (it & (NS - 1)) * STAGE_BYTES, lds + ((it + 1) & (NS - 1)) * STAGE_BYTES, jt0, none, IntTag<2>{});
         ++it;
         continue;
       }
     }
     sync_tile(it);
-    const char* St = lds + (it % NS) * STAGE_BYTES;
+    const char* St = lds + (it & (NS - 1)) * STAGE_BYTES;
     int act = 0;
     bool masked[QB] = {false, false};
     const int t = jt0 / BN;

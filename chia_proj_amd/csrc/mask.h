@@ -28,6 +28,33 @@ constexpr int32_t kInf = 1 << 29;  // band sentinel; seqlen is limited to < 2^28
 
 enum TileClass : int32_t { TILE_EMPTY = 0, TILE_FULL = 1, TILE_PARTIAL = 2 };
 
+// Division of a non-negative 31-bit n by a fixed d >= 1 as one multiply-high,
+// an add and a shift (Granlund & Montgomery, "Division by invariant integers
+// using multiplication", PLDI 1994, the round-up multiplier): with
+// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1 < 2^32,
+// n / d = (mulhi(m, n) + n) >> l, exact for 0 <= n < 2^31 (the sum stays
+// below 2^32).  The multiplier is computed on the host.
+struct UDiv {
+  uint32_t m;
+  int32_t l;
+};
+
+CHIA_HD UDiv make_udiv(int32_t d) {  // d >= 1 (host side: one 64-bit division)
+  int32_t l = 0;
+  while (((int64_t)1 << l) < d) ++l;
+  const uint64_t num = ((uint64_t)1 << 32) * (((uint64_t)1 << l) - (uint64_t)d);
+  return UDiv{(uint32_t)(num / (uint64_t)d + 1), l};
+}
+
+CHIA_HD int32_t udiv(int32_t n, UDiv f) {  // 0 <= n < 2^31
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t t = __umulhi(f.m, (uint32_t)n);
+#else
+  const uint32_t t = (uint32_t)(((uint64_t)f.m * (uint32_t)n) >> 32);
+#endif
+  return (int32_t)((t + (uint32_t)n) >> f.l);
+}
+
 // One residue class in sub-sequence coordinates.
 struct MaskGeom {
   int32_t S;       // sub-sequence length
@@ -35,6 +62,7 @@ struct MaskGeom {
   int32_t prefix;  // keys j' < prefix are visible to every query
   int32_t blk;     // block size in ORIGINAL positions, 0 = off
   int32_t dil, r;  // original position = r + dil * sub position
+  UDiv blk_div, dil_div;
 };
 
 CHIA_HD int32_t imax32(int32_t a, int32_t b) { return a > b ? a : b; }
@@ -54,8 +82,8 @@ CHIA_HD int32_t key_lo(const MaskGeom& g, int32_t i) {
   int32_t v = (g.hi >= kInf) ? 0 : i - g.hi;
   if (g.blk > 0) {
     const int32_t io = g.r + g.dil * i;
-    const int32_t bs = (io / g.blk) * g.blk;  // first original position of the block
-    v = imax32(v, bs <= g.r ? 0 : ceil_div(bs - g.r, g.dil));
+    const int32_t bs = udiv(io, g.blk_div) * g.blk;  // first original position of the block
+    v = imax32(v, bs <= g.r ? 0 : udiv(bs - g.r + g.dil - 1, g.dil_div));
   }
   return imax32(v, 0);
 }
@@ -65,8 +93,8 @@ CHIA_HD int32_t key_hi(const MaskGeom& g, int32_t i) {
   int32_t v = (g.lo <= -kInf) ? g.S - 1 : i - g.lo;
   if (g.blk > 0) {
     const int32_t io = g.r + g.dil * i;
-    const int32_t be = (io / g.blk) * g.blk + g.blk - 1;  // last original position
-    v = imin32(v, (be - g.r) / g.dil);                     // be >= io >= r
+    const int32_t be = udiv(io, g.blk_div) * g.blk + g.blk - 1;  // last original position
+    v = imin32(v, udiv(be - g.r, g.dil_div));                     // be >= io >= r
   }
   return imin32(v, g.S - 1);
 }
@@ -75,6 +103,21 @@ CHIA_HD bool visible(const MaskGeom& g, int32_t i, int32_t j) {
   if (j < 0 || j >= g.S || i < 0 || i >= g.S) return false;
   if (j < g.prefix) return true;
   return j >= key_lo(g, i) && j <= key_hi(g, i);
+}
+
+// Bits [a, b] of a 32-bit word (keys a..b counted from a block's first key),
+// clipped to [0, 31]; 0 when the range misses the word or is empty.
+CHIA_HD uint32_t key_bits(int32_t a, int32_t b) {
+  const int32_t lo = a < 0 ? 0 : (a > 32 ? 32 : a);
+  int32_t hi = b + 1 > 32 ? 32 : b + 1;
+  hi = hi < lo ? lo : hi;
+  return (uint32_t)(((uint64_t)1 << hi) - ((uint64_t)1 << lo));
+}
+
+// Keys jbase .. jbase + 31 that query i' does not see (also those past the
+// end), as bits 0..31: the per-element mask of a partly visible key block.
+CHIA_HD uint32_t hidden_bits(const MaskGeom& g, int32_t i, int32_t jbase) {
+  return ~(key_bits(key_lo(g, i) - jbase, key_hi(g, i) - jbase) | key_bits(-jbase, g.prefix - 1 - jbase));
 }
 
 // Classify queries [a, b] (a <= b <= S-1) against keys [c, d] (c <= S-1; d
@@ -169,6 +212,7 @@ struct MaskSpec {
   int32_t S;
   int32_t lo, hi;  // band in original units
   int32_t blk, prefix, dil;
+  UDiv blk_div, dil_div;  // dividers by blk (when > 0) and dil
 };
 
 CHIA_HD MaskSpec make_mask_spec(int32_t S, int32_t causal, int32_t window, int32_t dilation,
@@ -188,20 +232,28 @@ CHIA_HD MaskSpec make_mask_spec(int32_t S, int32_t causal, int32_t window, int32
   m.blk = block;
   m.prefix = prefix;
   m.dil = dilation < 1 ? 1 : dilation;
+  m.blk_div = make_udiv(block > 0 ? block : 1);
+  m.dil_div = make_udiv(m.dil);
   return m;
 }
 
 CHIA_HD int32_t num_residues(const MaskSpec& m) { return imin32(m.dil, m.S); }
 
+// Floor and ceiling of a / d for |a| < 2^30 with the divider of d.
+CHIA_HD int32_t floor_udiv(int32_t a, int32_t d, UDiv f) { return a >= 0 ? udiv(a, f) : -udiv(-a + d - 1, f); }
+CHIA_HD int32_t ceil_udiv(int32_t a, int32_t d, UDiv f) { return a >= 0 ? udiv(a + d - 1, f) : -udiv(-a, f); }
+
 CHIA_HD MaskGeom residue_geom(const MaskSpec& m, int32_t r) {
   MaskGeom g;
   g.dil = m.dil;
   g.r = r;
-  g.S = r < m.S ? (m.S - r + m.dil - 1) / m.dil : 0;
-  g.lo = m.lo <= -kInf ? -kInf : ceil_div(m.lo, m.dil);
-  g.hi = m.hi >= kInf ? kInf : floor_div(m.hi, m.dil);
+  g.S = r < m.S ? udiv(m.S - r + m.dil - 1, m.dil_div) : 0;
+  g.lo = m.lo <= -kInf ? -kInf : ceil_udiv(m.lo, m.dil, m.dil_div);
+  g.hi = m.hi >= kInf ? kInf : floor_udiv(m.hi, m.dil, m.dil_div);
   g.blk = m.blk;
-  const int32_t p = m.prefix > r ? ceil_div(m.prefix - r, m.dil) : 0;
+  g.blk_div = m.blk_div;
+  g.dil_div = m.dil_div;
+  const int32_t p = m.prefix > r ? udiv(m.prefix - r + m.dil - 1, m.dil_div) : 0;
   g.prefix = imin32(p, g.S);
   return g;
 }

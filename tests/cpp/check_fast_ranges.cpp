@@ -1,7 +1,8 @@
 // Brute-force check of fast_ranges and wide_range_all (chia_proj_amd/csrc/mask.h)
 // against classify_tile: every band key tile the kernel runs without
 // classification must have the class the fast path assumes, in every
-// wavefront for the workgroup-uniform WIDE span.  Built and run by
+// wavefront for the workgroup-uniform WIDE span; and of hidden_bits (the
+// per-element mask of partial blocks) against visible().  Built and run by
 // tests/test_mask_fast_ranges.py; exits non-zero on the first mismatch.
 #include <cstdio>
 #include <initializer_list>
@@ -10,8 +11,40 @@
 
 using namespace chia;
 
+// hidden_bits against visible() for every row and 4-aligned key base (the
+// kernel's blocks start at a tile + 32 kb + 4 lane-half)
+static int check_hidden_bits(long* n) {
+  for (int S : {1, 37, 65, 200, 513})
+    for (int causal = 0; causal < 2; ++causal)
+      for (int w : {0, 1, 5, 64, 129})
+        for (int d : {1, 2, 3})
+          for (int blk : {0, 33, 128})
+            for (int pre : {0, 40, 130}) {
+              if (d > 1 && pre > 0) continue;
+              const MaskSpec m = make_mask_spec(S, causal, w, d, blk, pre);
+              for (int r = 0; r < num_residues(m); ++r) {
+                const MaskGeom g = residue_geom(m, r);
+                for (int i = 0; i < g.S; ++i)
+                  for (int jb = 0; jb < g.S + 32; jb += 4) {
+                    const uint32_t h = hidden_bits(g, i, jb);
+                    for (int k = 0; k < 32; ++k) {
+                      ++*n;
+                      if (((h >> k) & 1u) == (uint32_t)visible(g, i, jb + k)) {
+                        std::printf("hidden_bits mismatch S=%d c=%d w=%d d=%d blk=%d p=%d r=%d i=%d j=%d\n", S, causal, w,
+                                    d, blk, pre, r, i, jb + k);
+                        return 1;
+                      }
+                    }
+                  }
+              }
+            }
+  return 0;
+}
+
 int main() {
   const int bn = 64;
+  long n_bits = 0;
+  if (check_hidden_bits(&n_bits)) return 1;
   long checked = 0, fast = 0, wide_all = 0;
   const int seqs[] = {1, 63, 64, 65, 200, 511, 700, 1024};
   const int windows[] = {0, 1, 5, 64, 129, 300};
@@ -93,6 +126,7 @@ int main() {
                 }
               }
             }
-  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span\n", checked, fast, wide_all);
+  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span, %ld mask bits\n", checked, fast,
+              wide_all, n_bits);
   return 0;
 }

@@ -1,6 +1,7 @@
-"""CPU check of the kernel's unclassified fast paths: fast_ranges
-(chia_proj_amd/csrc/mask.h) against classify_tile by brute force over masks,
-residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp)."""
+"""CPU checks of chia_proj_amd/csrc/mask.h by brute force: the kernel's
+unclassified fast paths (fast_ranges, wide_range_all) against classify_tile over
+masks, residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp), and
+the multiply-high divider against plain division (tests/cpp/check_udiv.cpp)."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -18,3 +19,13 @@ def test_fast_ranges_agree_with_classification(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "on a fast path" in out.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_udiv_matches_division(tmp_path):
+    exe = tmp_path / "check_udiv"
+    subprocess.run(["g++", "-std=c++17", "-O2", f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+                    str(ROOT / "tests" / "cpp" / "check_udiv.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "pairs" in out.stdout
