@@ -17,7 +17,7 @@ NORM_SIGMOID = 1
 NORM_RELU = 2
 NORMS = {"softmax": NORM_SOFTMAX, "sigmoid": NORM_SIGMOID, "relu": NORM_RELU}
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # Entry points declared in include/chia_attn.h (checked by the CPU tests).
 EXPORTS = (
@@ -61,7 +61,8 @@ class AttnArgs(ctypes.Structure):
         ("post_scale", ctypes.c_float),
         ("head_scale", ctypes.c_void_p),
         ("alibi_slopes", ctypes.c_void_p),
-        ("reserved", ctypes.c_int32 * 8),
+        ("kv_heads", ctypes.c_int32),
+        ("reserved", ctypes.c_int32 * 7),
     ]
 
     def __init__(self, **kw):

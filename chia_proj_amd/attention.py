@@ -120,6 +120,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
               out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Forward attention o = norm(mod(q k^T) | mask) @ v for bf16 [B, H, S, D] tensors.
 
+    k and v may have fewer heads than q ([B, H_kv, S, D], H_kv dividing H): query head h
+    then reads K/V head h // (H // H_kv) (grouped-query / multi-query attention).
+
     Mask: query i sees key j iff (j < prefix) or (band and block and dilation), with
     band = 0 <= i-j (< window) when causal, |i-j| < window otherwise (window=0: no limit),
     block: i//block == j//block, dilation: (i-j) % dilation == 0.
@@ -161,8 +164,10 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
             raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
     if q.dim() != 4:
         raise ValueError(f"q must be 4-D [B, H, S, D], got shape {tuple(q.shape)}")
-    if k.shape != q.shape or v.shape != q.shape:
-        raise ValueError(f"q, k, v must have the same shape, got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if (k.dim() != 4 or k.shape != v.shape or k.shape[0] != q.shape[0] or k.shape[2:] != q.shape[2:]
+            or k.shape[1] < 1 or q.shape[1] % k.shape[1] != 0):
+        raise ValueError(f"k and v must be [B, H_kv, S, D] with H_kv dividing q's H (GQA / MQA), got "
+                         f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise TypeError(f"q, k, v must be bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
     if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
@@ -200,6 +205,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
                   dilation=dilation, block=block, prefix=prefix, scale=sc, softcap=softcap, bias=bias,
                   post_scale=post_scale)
     a.q, a.k, a.v, a.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
+    a.kv_heads = k_.shape[1] if k_.shape[1] != H else 0
     for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
         st = getattr(a, name)
         st[0], st[1], st[2] = t.stride(0), t.stride(1), t.stride(2)

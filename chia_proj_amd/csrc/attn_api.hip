@@ -42,8 +42,9 @@ int validate(const chia_attn_args* a, bool need_tensors) {
   if (!(a->scale > 0.f) || !std::isfinite(a->scale)) return CHIA_ATTN_ERR_SCALE;
   if (!(a->softcap >= 0.f) || !std::isfinite(a->softcap)) return CHIA_ATTN_ERR_SCALE;
   if (!std::isfinite(a->bias) || !std::isfinite(a->post_scale)) return CHIA_ATTN_ERR_SCALE;
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 7; ++i)
     if (a->reserved[i] != 0) return CHIA_ATTN_ERR_STRUCT;
+  if (a->kv_heads < 0 || (a->kv_heads > 0 && a->heads % a->kv_heads != 0)) return CHIA_ATTN_ERR_SHAPE;
   if (need_tensors) {
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o)) return CHIA_ATTN_ERR_ALIGN;
     if (!stride_ok(a->q_stride) || !stride_ok(a->k_stride) || !stride_ok(a->v_stride) || !stride_ok(a->o_stride))
@@ -112,7 +113,8 @@ extern "C" const char* chia_attn_status_string(int status) {
     case CHIA_ATTN_OK: return "ok";
     case CHIA_ATTN_ERR_NULL: return "null argument, tensor or required per-head pointer";
     case CHIA_ATTN_ERR_SHAPE:
-      return "batch, heads and seqlen must be >= 1 (seqlen < 2^28); K/V seq strides in [0, 2^25 / dilation)";
+      return "batch, heads and seqlen must be >= 1 (seqlen < 2^28); K/V seq strides in [0, 2^25 / dilation); "
+             "kv_heads >= 0 and dividing heads";
     case CHIA_ATTN_ERR_HEAD_DIM: return "head_dim must be 64 or 128";
     case CHIA_ATTN_ERR_MASK: return "window, block and prefix must be >= 0, dilation >= 1, and prefix is not combinable with dilation > 1";
     case CHIA_ATTN_ERR_SCALE: return "scale must be finite and > 0; softcap finite and >= 0; bias, post_scale finite";
@@ -154,6 +156,7 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
   p.div_pairs = make_udiv(p.n_pairs);
   p.div_res = make_udiv(p.residues);
   p.div_h = make_udiv(p.H);
+  p.div_group = make_udiv(a->kv_heads > 0 ? (int32_t)(a->heads / a->kv_heads) : 1);
   p.scale = a->scale;
   p.softcap = a->softcap;
   p.bias = a->bias;

@@ -93,6 +93,7 @@ struct FwdParams {
   int32_t zigzag;             // pair blocks (i, n-1-i) instead of (2i, 2i+1)
   int32_t n_wg;
   UDiv div_pairs, div_res, div_h;  // dividers by n_pairs, residues, H
+  UDiv div_group;                  // by query heads per K/V head (GQA / MQA)
   float scale, softcap, bias, post_scale;
 };
 
@@ -253,8 +254,9 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
   const int dil = p.mask.dil;
   const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
-  const uint16_t* kh = p.k + b * p.k_sb + h * p.k_sh + r * p.k_ss;
-  const uint16_t* vh = p.v + b * p.v_sb + h * p.v_sh + r * p.v_ss;
+  const int hk = udiv(h, p.div_group);  // K/V head of query head h
+  const uint16_t* kh = p.k + b * p.k_sb + hk * p.k_sh + r * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hk * p.v_sh + r * p.v_ss;
   uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + r * p.o_ss;
   const int64_t qrs = p.q_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil, ors = p.o_ss * dil;
 

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define CHIA_ATTN_ABI_VERSION 1
+#define CHIA_ATTN_ABI_VERSION 2  /* 2: kv_heads (GQA / MQA) */
 
 /* Normaliser applied to the (modified, masked) scores.
  *   SOFTMAX: p = softmax_j(s) over visible keys   (extra_bench.py:42)
@@ -47,8 +47,9 @@ enum chia_attn_norm {
 enum chia_attn_status {
   CHIA_ATTN_OK = 0,
   CHIA_ATTN_ERR_NULL = -1,          /* NULL args, tensor or required pointer */
-  CHIA_ATTN_ERR_SHAPE = -2,         /* batch/heads/seqlen < 1 or too large, or a K/V seq
-                                        stride < 0 or >= 2^25 / dilation elements      */
+  CHIA_ATTN_ERR_SHAPE = -2,         /* batch/heads/seqlen < 1 or too large, a K/V seq
+                                        stride < 0 or >= 2^25 / dilation elements, or
+                                        kv_heads < 0 or not dividing heads              */
   CHIA_ATTN_ERR_HEAD_DIM = -3,      /* head_dim not in {64, 128}            */
   CHIA_ATTN_ERR_MASK = -4,          /* negative window/block/prefix, dilation < 1,
                                        or prefix > 0 with dilation > 1 */
@@ -63,8 +64,8 @@ typedef struct chia_attn_args {
   uint32_t norm;          /* enum chia_attn_norm */
 
   const void* q;          /* bf16 [B, H, S, D] */
-  const void* k;          /* bf16 [B, H, S, D] */
-  const void* v;          /* bf16 [B, H, S, D] */
+  const void* k;          /* bf16 [B, H_kv, S, D] (H_kv = kv_heads, or H) */
+  const void* v;          /* bf16 [B, H_kv, S, D] */
   void* o;                /* bf16 [B, H, S, D], written */
 
   int64_t batch, heads, seqlen, head_dim;
@@ -97,7 +98,12 @@ typedef struct chia_attn_args {
   const float* head_scale;    /* device float[heads] or NULL (extra_bench.py:35,54) */
   const float* alibi_slopes;  /* device float[heads] or NULL (extra_bench.py:36,47-50) */
 
-  int32_t reserved[8];        /* must be zero */
+  /* Grouped-query / multi-query attention: K and V have kv_heads heads and
+   * query head h reads K/V head h / (heads / kv_heads).  0 = heads (one K/V
+   * head per query head).  heads % kv_heads must be 0.  The reference's
+   * kernels take K and V of q's shape only; this generalises them. */
+  int32_t kv_heads;
+  int32_t reserved[7];        /* must be zero */
 } chia_attn_args;
 
 /* Launch one forward attention on `stream` (a hipStream_t; NULL = default

@@ -51,6 +51,11 @@ def attention_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: st
     hs = None if head_scale is None else torch.as_tensor(head_scale, dtype=dtype).reshape(H).cpu()
     sl = None if alibi_slopes is None else torch.as_tensor(alibi_slopes, dtype=dtype).reshape(H).cpu()
     qf, kf, vf = (t.detach().to("cpu", dtype) for t in (q, k, v))
+    if kf.shape[1] != H:  # grouped-query / multi-query: query head h reads K/V head h // (H // H_kv)
+        if H % kf.shape[1] or vf.shape != kf.shape:
+            raise ValueError(f"K/V heads {kf.shape[1]} must divide query heads {H}")
+        kf = kf.repeat_interleave(H // kf.shape[1], dim=1)
+        vf = vf.repeat_interleave(H // vf.shape[1], dim=1)
     out = torch.empty(B, H, S, D, dtype=dtype)
     for b in range(B):
         for h0 in range(0, H, heads_per_chunk):

@@ -81,6 +81,11 @@ def test_cpu_tensors_are_rejected_not_computed():
     (lambda: attention(torch.zeros(1, 2, 64, 64), torch.zeros(1, 2, 64, 64), torch.zeros(1, 2, 64, 64)), TypeError),
     (lambda: attention(*(torch.zeros(2, 64, 64, dtype=torch.bfloat16),) * 3), ValueError),
     (lambda: attention(*(torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16),) * 3, norm="tanh"), ValueError),
+    # K/V heads must divide the query heads, and K and V must agree
+    (lambda: attention(torch.zeros(1, 6, 64, 64, dtype=torch.bfloat16), *(torch.zeros(1, 4, 64, 64, dtype=torch.bfloat16),) * 2),
+     ValueError),
+    (lambda: attention(torch.zeros(1, 4, 64, 64, dtype=torch.bfloat16), torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16),
+                       torch.zeros(1, 1, 64, 64, dtype=torch.bfloat16)), ValueError),
 ])
 def test_validation_errors(bad, exc):
     with pytest.raises(exc):

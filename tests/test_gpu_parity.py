@@ -224,3 +224,32 @@ def test_cached_launch_path_follows_new_data():
         r = oracle.attention_ref(qq, k, v, causal=True, window=77, head_scale=t.cpu())
         res = gate.north_star_gate(r, o.float().cpu())
         assert res.ok, res.stats
+
+
+GQA_CASES = [
+    # (name, H, H_kv, S, D, generic kwargs)
+    ("causal_g2", 8, 4, 640, 64, dict(causal=True)),
+    ("window_g4", 8, 2, 700, 64, dict(causal=True, window=100)),
+    ("mqa_alibi", 8, 1, 513, 64, dict(causal=True, alibi_slopes=[0.5 ** (h + 1) for h in range(8)])),
+    ("sigmoid_full_g2", 4, 2, 384, 128, dict(norm="sigmoid", causal=False, bias=-2.0)),
+    ("relu_block_g4", 4, 1, 300, 64, dict(norm="relu", causal=True, block=64, post_scale=0.05)),
+    ("softcap_prefix_g2", 4, 2, 333, 128, dict(causal=True, prefix=70, softcap=20.0)),
+]
+
+
+@pytest.mark.parametrize("name,H,Hkv,S,D,kw", GQA_CASES, ids=[c[0] for c in GQA_CASES])
+def test_grouped_query_kv(name, H, Hkv, S, D, kw):
+    """K/V with fewer heads than Q (GQA / MQA): bit-identical to the same call with each
+    K/V head repeated for its query heads, and within the gate of the oracle."""
+    _say(f"[parity] gqa {name}")
+    g = torch.Generator("cpu").manual_seed(H * 1000 + Hkv * 10 + S)
+    q = torch.randn(2, H, S, D, generator=g).to(torch.bfloat16)
+    k, v = (torch.randn(2, Hkv, S, D, generator=g).to(torch.bfloat16) for _ in range(2))
+    o = attention(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+    rep = H // Hkv
+    o_rep = attention(q.to(DEV), k.repeat_interleave(rep, 1).to(DEV), v.repeat_interleave(rep, 1).to(DEV), **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_rep), name
+    r = oracle.attention_ref(q, k, v, **kw)
+    res = gate.north_star_gate(r, o.float().cpu(), scale_aware=kw.get("norm", "softmax") != "softmax")
+    assert res.ok, f"{name}: {res.status} {res.stats}"

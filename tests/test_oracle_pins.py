@@ -302,3 +302,17 @@ def test_planted_masked_before_sigmoid_is_rejected():
     expect = 0.5 * (ok @ v[0, 0])
     assert torch.allclose(variant_ref("sigmoid_attn", qz, k, v, dtype=F64)[0, 0], expect, atol=1e-12)
     assert not torch.allclose(buggy(qz, k, v)[0, 0], expect, atol=1e-3)
+
+
+@pytest.mark.parametrize("H,Hkv", [(4, 2), (6, 1), (8, 4)])
+def test_grouped_query_oracle_equals_sdpa_gqa(H, Hkv):
+    """The oracle's grouped-query path (query head h reads K/V head h // (H // H_kv))
+    against torch's own GQA implementation (scaled_dot_product_attention, enable_gqa)."""
+    g = torch.Generator().manual_seed(H * 31 + Hkv)
+    q = torch.randn(2, H, 80, 32, generator=g, dtype=torch.float64)
+    k, v = (torch.randn(2, Hkv, 80, 32, generator=g, dtype=torch.float64) for _ in range(2))
+    for causal, window in ((True, 0), (True, 11), (False, 0)):
+        mask = visible_mask(80, causal=causal, window=window)
+        want = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True)
+        got = attention_ref(q, k, v, causal=causal, window=window, dtype=torch.float64)
+        torch.testing.assert_close(got, want, rtol=1e-10, atol=1e-10)
