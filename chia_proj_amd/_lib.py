@@ -22,6 +22,9 @@ ABI_VERSION = 2
 # Entry points declared in include/chia_attn.h (checked by the CPU tests).
 EXPORTS = (
     "chia_attn_fwd",
+    "chia_attn_fwd_lse",
+    "chia_attn_bwd",
+    "chia_attn_bwd_workspace_size",
     "chia_attn_plan",
     "chia_attn_tile_map",
     "chia_attn_query_intervals",
@@ -74,6 +77,34 @@ class AttnArgs(ctypes.Structure):
             setattr(self, key, val)
 
 
+class BwdArgs(ctypes.Structure):
+    """Mirror of ``chia_attn_bwd_args``."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("reserved0", ctypes.c_uint32),
+        ("fwd", ctypes.POINTER(AttnArgs)),
+        ("dout", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("dout_stride", _i64x3),
+        ("dq_stride", _i64x3),
+        ("dk_stride", _i64x3),
+        ("dv_stride", _i64x3),
+        ("lse", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+        ("reserved", ctypes.c_int32 * 8),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(BwdArgs)
+        for key, val in kw.items():
+            setattr(self, key, val)
+
+
 class PlanInfo(ctypes.Structure):
     """Mirror of ``chia_attn_plan_info``."""
 
@@ -121,6 +152,12 @@ def _load():
         lib = ctypes.CDLL(str(LIB_PATH))
         lib.chia_attn_fwd.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p]
         lib.chia_attn_fwd.restype = ctypes.c_int
+        lib.chia_attn_fwd_lse.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_void_p]
+        lib.chia_attn_fwd_lse.restype = ctypes.c_int
+        lib.chia_attn_bwd.argtypes = [ctypes.POINTER(BwdArgs), ctypes.c_void_p]
+        lib.chia_attn_bwd.restype = ctypes.c_int
+        lib.chia_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
+        lib.chia_attn_bwd_workspace_size.restype = ctypes.c_int64
         lib.chia_attn_plan.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(PlanInfo)]
         lib.chia_attn_plan.restype = ctypes.c_int
         lib.chia_attn_tile_map.argtypes = [
@@ -156,6 +193,25 @@ def fwd(args: AttnArgs, stream: int) -> None:
     st = _load().chia_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
     if st != 0:
         raise ChiaAttnError(st, "chia_attn_fwd")
+
+
+def fwd_lse(args: AttnArgs, lse_ptr: int, stream: int) -> None:
+    st = _load().chia_attn_fwd_lse(ctypes.byref(args), ctypes.c_void_p(lse_ptr), ctypes.c_void_p(stream))
+    if st != 0:
+        raise ChiaAttnError(st, "chia_attn_fwd_lse")
+
+
+def bwd_workspace_size(args: AttnArgs) -> int:
+    n = _load().chia_attn_bwd_workspace_size(ctypes.byref(args))
+    if n < 0:
+        raise ChiaAttnError(int(n), "chia_attn_bwd_workspace_size")
+    return int(n)
+
+
+def bwd(args: BwdArgs, stream: int) -> None:
+    st = _load().chia_attn_bwd(ctypes.byref(args), ctypes.c_void_p(stream))
+    if st != 0:
+        raise ChiaAttnError(st, "chia_attn_bwd")
 
 
 def plan(args: AttnArgs) -> dict:

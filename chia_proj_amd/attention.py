@@ -10,6 +10,7 @@ leaves synchronisation to the caller, extra_bench.py:12,19).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import threading
 from collections import OrderedDict
@@ -130,6 +131,13 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
     softcap * tanh(s / softcap) when softcap > 0.
     norm: "softmax" | "sigmoid" (sigmoid(s + bias) * post_scale) | "relu" (relu(s) * post_scale).
     """
+    params = dict(norm=norm, causal=causal, window=window, dilation=dilation, block=block, prefix=prefix,
+                  scale=scale, head_scale=head_scale, alibi_slopes=alibi_slopes, softcap=softcap, bias=bias,
+                  post_scale=post_scale)
+    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v)):
+        if out is not None:
+            raise ValueError("out= is not supported when q, k or v requires grad")
+        return _AttentionFn.apply(q, k, v, params)
     # Fast path: a call with the same shapes, layouts and parameters as an
     # earlier one reuses its validated argument struct and per-head vectors;
     # only the data pointers (and their alignment) are new.
@@ -159,6 +167,22 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
             _lib.fwd(a, torch.cuda.current_stream(q.device).cuda_stream)
             return o
 
+    a, hs, sl, (q_, k_, v_), o = _prepare(q, k, v, out, **params)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        _lib.fwd(a, stream)
+    # Cache the validated call when the tensors needed no layout change and a
+    # fresh output would get the same strides as this one.
+    if key is not None and q_ is q and k_ is k and v_ is v and (out is not None or o.stride() == q.stride()):
+        cache[key] = (a, hs, sl)
+        if len(cache) > _ARGS_CACHE_MAX:
+            cache.popitem(last=False)
+    return o
+
+
+def _prepare(q, k, v, out, *, norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes,
+             softcap, bias, post_scale):
+    """Validate, make the layouts the kernel takes, allocate o and fill the argument struct."""
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
@@ -211,16 +235,50 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
         st[0], st[1], st[2] = t.stride(0), t.stride(1), t.stride(2)
     a.head_scale = hs.data_ptr() if hs is not None else None
     a.alibi_slopes = sl.data_ptr() if sl is not None else None
-    with torch.cuda.device(q.device):
-        stream = torch.cuda.current_stream(q.device).cuda_stream
-        _lib.fwd(a, stream)
-    # Cache the validated call when the tensors needed no layout change and a
-    # fresh output would get the same strides as this one.
-    if key is not None and q_ is q and k_ is k and v_ is v and (out is not None or o.stride() == q.stride()):
-        cache[key] = (a, hs, sl)
-        if len(cache) > _ARGS_CACHE_MAX:
-            cache.popitem(last=False)
-    return o
+    return a, hs, sl, (q_, k_, v_), o
+
+
+def _strides3(t: torch.Tensor):
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+class _AttentionFn(torch.autograd.Function):
+    """attention() with gradients: the forward also keeps the softmax log-sum-exp
+    (chia_attn_fwd_lse); the backward launches chia_attn_bwd (dq, dk, dv; the
+    per-head vectors, softcap, bias and post_scale are constants)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, params):
+        a, hs, sl, (q_, k_, v_), o = _prepare(q, k, v, None, **params)
+        B, H, S, _ = q_.shape
+        lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device) if params["norm"] == "softmax" else None
+        with torch.cuda.device(q.device):
+            stream = torch.cuda.current_stream(q.device).cuda_stream
+            _lib.fwd_lse(a, lse.data_ptr() if lse is not None else 0, stream)
+        ctx.params = params
+        ctx.vecs = (hs, sl)  # the device vectors the argument struct points at
+        ctx.save_for_backward(q_, k_, v_, o, *(() if lse is None else (lse,)))
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q_, k_, v_, o, *rest = ctx.saved_tensors
+        lse = rest[0] if rest else None
+        a, _, _, _, _ = _prepare(q_, k_, v_, o, **ctx.params)
+        do_ = do if (do.dtype == torch.bfloat16 and _layout_ok(do)) else do.to(torch.bfloat16).contiguous()
+        dq, dk, dv = torch.empty_like(q_), torch.empty_like(k_), torch.empty_like(v_)
+        nbytes = _lib.bwd_workspace_size(a)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q_.device)
+        b = _lib.BwdArgs(dout=do_.data_ptr(), dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
+                         lse=lse.data_ptr() if lse is not None else None, workspace=ws.data_ptr(),
+                         workspace_bytes=nbytes)
+        b.fwd = ctypes.pointer(a)
+        for name, t in (("dout_stride", do_), ("dq_stride", dq), ("dk_stride", dk), ("dv_stride", dv)):
+            st = getattr(b, name)
+            st[0], st[1], st[2] = _strides3(t)
+        with torch.cuda.device(q_.device):
+            _lib.bwd(b, torch.cuda.current_stream(q_.device).cuda_stream)
+        return dq, dk, dv, None
 
 
 def plan(*, batch: int, heads: int, seqlen: int, head_dim: int, **mask_kw) -> dict:

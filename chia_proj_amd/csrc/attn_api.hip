@@ -10,7 +10,7 @@
 #include <cmath>
 #include <cstring>
 
-#include "attn_fwd_kernel.h"
+#include "attn_bwd_kernel.h"
 #include "chia_attn.h"
 
 namespace chia {
@@ -18,6 +18,8 @@ namespace chia {
 using KernelFn = void (*)(FwdParams);
 KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
 KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap);
+BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
+BwdKernels select_bwd_kernels_d128(int norm, bool alibi, bool softcap);
 
 namespace {
 
@@ -121,15 +123,18 @@ extern "C" const char* chia_attn_status_string(int status) {
     case CHIA_ATTN_ERR_NORM: return "unknown normaliser";
     case CHIA_ATTN_ERR_ALIGN: return "tensors must be 16-byte aligned with batch/head/seq strides multiple of 8 elements";
     case CHIA_ATTN_ERR_STRUCT: return "struct_size mismatch or reserved fields not zero";
+    case CHIA_ATTN_ERR_WORKSPACE: return "backward workspace NULL or smaller than chia_attn_bwd_workspace_size";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "unknown status";
 }
 
-extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
+namespace {
+int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   const int st = validate(a, true);
   if (st != CHIA_ATTN_OK) return st;
+  if ((uintptr_t)lse & 3u) return CHIA_ATTN_ERR_ALIGN;
 
   FwdParams p;
   std::memset(&p, 0, sizeof(p));
@@ -161,6 +166,7 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
   p.softcap = a->softcap;
   p.bias = a->bias;
   p.post_scale = a->post_scale;
+  p.lse = a->norm == CHIA_ATTN_NORM_SOFTMAX ? lse : nullptr;
 
   bool alibi = a->alibi_slopes != nullptr;
   const bool softcap = a->softcap > 0.f;
@@ -176,6 +182,126 @@ extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) {
                                    0, (hipStream_t)stream);
   if (err != hipSuccess) return (int)err;
   err = hipGetLastError();
+  return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
+}
+}  // namespace
+
+extern "C" int chia_attn_fwd(const chia_attn_args* a, void* stream) { return launch_fwd(a, nullptr, stream); }
+
+extern "C" int chia_attn_fwd_lse(const chia_attn_args* a, float* lse, void* stream) {
+  if (lse == nullptr && a != nullptr && a->norm == CHIA_ATTN_NORM_SOFTMAX) return CHIA_ATTN_ERR_NULL;
+  return launch_fwd(a, lse, stream);
+}
+
+namespace {
+constexpr int kBwdMaxGroup = 256;  // query heads per K/V head the dK/dV kernel stages
+constexpr int kBwdBlock = 128;     // rows (dQ) or keys (dK/dV) per workgroup
+
+// Rows of the stats workspace per (b, h, residue): residue 0's length padded
+// to the 64-row tiles the dK/dV kernel reads whole.
+int64_t stats_rows(const MaskSpec& m) { return ((int64_t)residue_geom(m, 0).S + 63) / 64 * 64; }
+
+int64_t bwd_workspace(const chia_attn_args* a) {
+  if (a->norm != CHIA_ATTN_NORM_SOFTMAX) return 0;
+  const MaskSpec m = spec_of(a);
+  return 2 * a->batch * a->heads * (int64_t)num_residues(m) * stats_rows(m) * (int64_t)sizeof(float);
+}
+
+hipError_t launch(BwdKernelFn fn, int64_t grid, const BwdParams& p, hipStream_t stream) {
+  if (grid <= 0) return hipSuccess;
+  BwdParams q = p;
+  q.n_wg = (int32_t)grid;
+  void* kargs[] = {&q};
+  const hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)grid), dim3(256), kargs, 0, stream);
+  return err != hipSuccess ? err : hipGetLastError();
+}
+}  // namespace
+
+extern "C" int64_t chia_attn_bwd_workspace_size(const chia_attn_args* a) {
+  const int st = validate(a, false);
+  return st != CHIA_ATTN_OK ? st : bwd_workspace(a);
+}
+
+extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
+  if (!ba) return CHIA_ATTN_ERR_NULL;
+  if (ba->struct_size != sizeof(chia_attn_bwd_args) || ba->reserved0 != 0) return CHIA_ATTN_ERR_STRUCT;
+  for (int i = 0; i < 8; ++i)
+    if (ba->reserved[i] != 0) return CHIA_ATTN_ERR_STRUCT;
+  const chia_attn_args* a = ba->fwd;
+  const int st = validate(a, true);
+  if (st != CHIA_ATTN_OK) return st;
+  if (!ba->dout || !ba->dq || !ba->dk || !ba->dv) return CHIA_ATTN_ERR_NULL;
+  if (!aligned16(ba->dout) || !aligned16(ba->dq) || !aligned16(ba->dk) || !aligned16(ba->dv)) return CHIA_ATTN_ERR_ALIGN;
+  if (!stride_ok(ba->dout_stride) || !stride_ok(ba->dq_stride) || !stride_ok(ba->dk_stride) || !stride_ok(ba->dv_stride))
+    return CHIA_ATTN_ERR_ALIGN;
+  // Q and dO tiles are streamed like K and V: 32-bit row offsets within a tile
+  for (const int64_t* s : {a->q_stride, ba->dout_stride})
+    if (s[2] < 0 || s[2] * a->dilation >= kMaxKvRowStride) return CHIA_ATTN_ERR_SHAPE;
+  const bool softmax = a->norm == CHIA_ATTN_NORM_SOFTMAX;
+  if (softmax) {
+    if (!ba->lse) return CHIA_ATTN_ERR_NULL;
+    if ((uintptr_t)ba->lse & 3u) return CHIA_ATTN_ERR_ALIGN;
+    if (!ba->workspace || ba->workspace_bytes < bwd_workspace(a) || ((uintptr_t)ba->workspace & 15u))
+      return CHIA_ATTN_ERR_WORKSPACE;
+  }
+  const int64_t hkv = a->kv_heads > 0 ? a->kv_heads : a->heads;
+  const int64_t G = a->heads / hkv;
+  if (G > kBwdMaxGroup) return CHIA_ATTN_ERR_SHAPE;
+
+  BwdParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = (const uint16_t*)a->q;
+  p.k = (const uint16_t*)a->k;
+  p.v = (const uint16_t*)a->v;
+  p.o = (const uint16_t*)a->o;
+  p.dout = (const uint16_t*)ba->dout;
+  p.dq = (uint16_t*)ba->dq;
+  p.dk = (uint16_t*)ba->dk;
+  p.dv = (uint16_t*)ba->dv;
+  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
+  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
+  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
+  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.do_sb = ba->dout_stride[0]; p.do_sh = ba->dout_stride[1]; p.do_ss = ba->dout_stride[2];
+  p.dq_sb = ba->dq_stride[0]; p.dq_sh = ba->dq_stride[1]; p.dq_ss = ba->dq_stride[2];
+  p.dk_sb = ba->dk_stride[0]; p.dk_sh = ba->dk_stride[1]; p.dk_ss = ba->dk_stride[2];
+  p.dv_sb = ba->dv_stride[0]; p.dv_sh = ba->dv_stride[1]; p.dv_ss = ba->dv_stride[2];
+  p.lse = softmax ? ba->lse : nullptr;
+  p.stats = softmax ? (float*)ba->workspace : nullptr;
+  p.head_scale = a->head_scale;
+  p.alibi_slopes = a->alibi_slopes;
+  p.mask = spec_of(a);
+  p.B = (int32_t)a->batch;
+  p.H = (int32_t)a->heads;
+  p.G = (int32_t)G;
+  p.residues = num_residues(p.mask);
+  p.SR = (int32_t)stats_rows(p.mask);
+  p.n_blk = (residue_geom(p.mask, 0).S + kBwdBlock - 1) / kBwdBlock;
+  p.div_blk = make_udiv(p.n_blk);
+  p.div_res = make_udiv(p.residues);
+  p.div_h = make_udiv(p.H);
+  p.div_g = make_udiv(p.G);
+  p.div_hk = make_udiv((int32_t)hkv);
+  p.div_dil = make_udiv(p.mask.dil);
+  p.scale = a->scale;
+  p.softcap = a->softcap;
+  p.bias = a->bias;
+  p.post_scale = a->post_scale;
+
+  const int64_t rows = a->batch * a->heads * a->seqlen;
+  const int64_t g_stats = (rows + 255) / 256;
+  const int64_t g_dq = a->batch * a->heads * p.residues * (int64_t)p.n_blk;
+  const int64_t g_dkdv = a->batch * hkv * p.residues * (int64_t)p.n_blk;
+  if (g_stats >= ((int64_t)1 << 31) || g_dq >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
+
+  const bool alibi = a->alibi_slopes != nullptr, softcap = a->softcap > 0.f;
+  const BwdKernels ks = a->head_dim == 64 ? select_bwd_kernels_d64((int)a->norm, alibi, softcap)
+                                          : select_bwd_kernels_d128((int)a->norm, alibi, softcap);
+  const hipStream_t s = (hipStream_t)stream;
+  hipError_t err = hipSuccess;
+  if (softmax) err = launch(ks.stats, g_stats, p, s);
+  if (err == hipSuccess) err = launch(ks.dq, g_dq, p, s);
+  if (err == hipSuccess) err = launch(ks.dkdv, g_dkdv, p, s);
   return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
 }
 

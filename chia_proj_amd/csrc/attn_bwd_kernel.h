@@ -1,0 +1,536 @@
+// attn_bwd_kernel.h -- gfx950 backward of the attention core: dQ, dK, dV.
+//
+// Semantics: the gradient of the forward in attn_fwd_kernel.h with respect to
+// q, k and v (per-head scale, ALiBi slopes and the softcap are constants).
+// Per score, with u = (q.k) c1 + slope (j - i), t = softcap tanh(u / softcap)
+// (or u), p the normaliser's output and dp = do.v:
+//   softmax  p = exp(t - lse_i),            dt = p (dp - delta_i),
+//            delta_i = do_i . o_i
+//   sigmoid  p = post sigma(t + bias),      dt = dp post sigma (1 - sigma)
+//   ReLU     p = post max(t, 0),            dt = dp post [t > 0]
+//   ds = dt (dt/du) c1,  dt/du = 1 - tanh^2 with a softcap, else 1
+//   dV_j = sum_i p_ij do_i,  dK_j = sum_i ds_ij q_i,  dQ_i = sum_j ds_ij k_j
+// Masked pairs have p = ds = 0.  The reference is forward-only; this follows
+// the textbook derivation (autograd of the same formula is the oracle).
+//
+// Three launches, no atomics:
+//   * attn_bwd_stats_kernel: per row, lse log2 e and delta, into a workspace
+//     laid out per dilation residue (contiguous rows for the two kernels);
+//   * attn_bwd_dq_kernel: a workgroup owns 128 query rows (32 per wavefront)
+//     and streams the K / V tiles of their key range -- the forward's layout:
+//     S^T = K Q^T and dP^T = V dO^T with Q, dO in registers, dS^T from the
+//     lane's row statistics, dQ^T += K^T dS^T with K read transposed;
+//   * attn_bwd_dkdv_kernel: a workgroup owns 128 keys (32 per wavefront) of
+//     one K/V head and streams the Q / dO tiles of the rows that see them, for
+//     every query head of the group (GQA): S = Q K^T and dP = dO V^T with K, V
+//     in registers (lane = key), dV^T += dO^T P and dK^T += Q^T dS with Q and
+//     dO read transposed.
+// Tiles are 64 rows, DMA'd HBM -> LDS as in the forward (one swizzle for both
+// the row and the transposed reads), three LDS stages, one barrier per tile.
+#pragma once
+#include "attn_fwd_kernel.h"
+
+namespace chia {
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// 4-byte-per-lane HBM -> LDS DMA (uniform base + per-lane byte offset; lane l
+// lands at lds_base + 4 l), ordered by the kernel's own vmcnt waits like
+// dma16s.
+__device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  const uint64_t v = (uint64_t)(uintptr_t)sbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+  const uint64_t u = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(u), "{m0}"(lds_base) : "memory");
+}
+
+struct BwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t q_sb, q_sh, q_ss;  // element strides: batch, head, seq
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int64_t do_sb, do_sh, do_ss;
+  int64_t dq_sb, dq_sh, dq_ss;
+  int64_t dk_sb, dk_sh, dk_ss;
+  int64_t dv_sb, dv_sh, dv_ss;
+  const float* lse;     // softmax: [B, H, S], natural log
+  float* stats;         // softmax: [B, H, R, SR] lse log2 e, then [B, H, R, SR] delta
+  const float* head_scale;
+  const float* alibi_slopes;
+  MaskSpec mask;
+  int32_t B, H, G;      // G: query heads per K/V head
+  int32_t residues, SR;  // SR: stats row stride (residue 0 length, padded)
+  int32_t n_blk, n_wg;  // 128-row (or key) blocks per (b, head, residue 0); grid
+  UDiv div_blk, div_res, div_h, div_g, div_hk, div_dil;
+  float scale, softcap, bias, post_scale;
+};
+
+// Per-score gradient (see the header): from the raw s = q.k, dp = do.v and
+// j - i, the probability p (for dV) and ds (for dQ, dK).
+template <int NORM, bool ALIBI, bool SOFTCAP>
+struct ScoreGrad {
+  float c1, sl, cap, k2cap, post, nbias_l2;
+
+  __device__ __forceinline__ void operator()(float s, float dp, float jmi, float lse2, float delta, float& p,
+                                             float& ds) const {
+    float u = s * c1;
+    if constexpr (ALIBI) u = __builtin_fmaf(sl, jmi, u);
+    float t = u, dtdu = 1.0f;
+    if constexpr (SOFTCAP) {
+      // tanh(u / cap) = 1 - 2 / (1 + 2^(2 u log2e / cap))
+      const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * k2cap));
+      t = cap * th;
+      dtdu = __builtin_fmaf(-th, th, 1.0f);
+    }
+    float dt;
+    if constexpr (NORM == NORM_SOFTMAX) {
+      p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, kLog2e, -lse2));
+      dt = p * (dp - delta);
+    } else if constexpr (NORM == NORM_SIGMOID) {
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(-t, kLog2e, nbias_l2)));
+      p = post * sg;
+      dt = dp * p * (1.0f - sg);
+    } else {
+      p = post * fmaxf(t, 0.0f);
+      dt = t > 0.0f ? dp * post : 0.0f;
+    }
+    ds = dt * dtdu * c1;
+  }
+};
+
+// The per-call constants (no memory access); c1 and sl are the query head's
+// scale * head_scale and ALiBi slope per sub-sequence step, set by the caller.
+template <int NORM, bool ALIBI, bool SOFTCAP>
+__device__ __forceinline__ ScoreGrad<NORM, ALIBI, SOFTCAP> score_consts(const BwdParams& p) {
+  ScoreGrad<NORM, ALIBI, SOFTCAP> f;
+  f.c1 = p.scale;
+  f.sl = 0.0f;
+  f.cap = p.softcap;
+  f.k2cap = SOFTCAP ? 2.0f * kLog2e / p.softcap : 0.0f;
+  f.post = p.post_scale;
+  f.nbias_l2 = -p.bias * kLog2e;
+  return f;
+}
+
+// One 64-row tile of a [S, D] bf16 tensor (row stride rs elements, rows from
+// `row` of the residue's sub-sequence, clamped to S - 1) into LDS at `dst`:
+// row r, 16-byte chunk c lands in slot c ^ (r & 7).  Wavefront w of NW moves
+// chunks [(n NW + w) 64, +64) for n < NDMA.
+template <int D, int NW>
+__device__ __forceinline__ void dma_rows(const uint16_t* base, int64_t rs, int row, int S, char* dst, int wave,
+                                         int lane) {
+  constexpr int DQ = D / 8;
+  constexpr int NDMA = 64 * DQ / (NW * 64);
+  const uint16_t* src = base + (int64_t)row * rs;
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int pos = (n * NW + wave) * 64 + lane;
+    const int r = pos / DQ, slot = pos % DQ;
+    const int rr = imin32(r, S - 1 - row);
+    dma16s(src, (uint32_t)(2 * ((int64_t)rr * rs + 8 * k_slot(r, slot))), lds_addr(dst + (n * NW + wave) * 1024));
+  }
+}
+
+// Kernel set of one (head_dim, normaliser, ALiBi, softcap) instantiation.
+using BwdKernelFn = void (*)(BwdParams);
+struct BwdKernels {
+  BwdKernelFn stats, dq, dkdv;
+};
+
+// ---- row statistics ----------------------------------------------------------
+// One thread per (b, h, row): lse log2 e and delta = do . o, stored at
+// [b, h, residue, row / dil] so each residue's rows are contiguous.
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdParams p) {
+  const int S = p.mask.S;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.B * p.H * S) return;
+  const int bh = (int)(idx / S);
+  const int i = (int)(idx - (int64_t)bh * S);
+  const int b = udiv(bh, p.div_h), h = bh - b * p.H;
+  const uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)i * p.o_ss;
+  const uint16_t* drow = p.dout + b * p.do_sb + h * p.do_sh + (int64_t)i * p.do_ss;
+  float acc = 0.f;
+#pragma unroll
+  for (int c = 0; c < D / 8; ++c) {
+    const u32x4_t ov = *(const u32x4_t*)(orow + 8 * c);
+    const u32x4_t dv = *(const u32x4_t*)(drow + 8 * c);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      acc = __builtin_fmaf(__uint_as_float(ov[w] << 16), __uint_as_float(dv[w] << 16), acc);
+      acc = __builtin_fmaf(__uint_as_float(ov[w] & 0xffff0000u), __uint_as_float(dv[w] & 0xffff0000u), acc);
+    }
+  }
+  const int ir = udiv(i, p.div_dil), r = i - ir * p.mask.dil;
+  const int64_t o2 = ((int64_t)bh * p.residues + r) * p.SR + ir;
+  const int64_t plane = (int64_t)p.B * p.H * p.residues * p.SR;
+  p.stats[o2] = p.lse[idx] * kLog2e;
+  p.stats[plane + o2] = acc;
+}
+
+// ---- dQ ------------------------------------------------------------------------
+template <int D, int NORM, bool ALIBI, bool SOFTCAP>
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const BwdParams p) {
+  constexpr int NW = 4, BN = 64, KB = BN / 32, DK = D / 16, DB = D / 32;
+  constexpr int RP = 2 * D, T_BYTES = BN * RP, STAGE_BYTES = 2 * T_BYTES;
+  constexpr int NS = 3;
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, lh = lane >> 5;
+
+  // workgroup -> (b, h, residue, 128-row block), heaviest blocks first
+  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  const int bhr = udiv(L, p.div_blk);
+  const int blk = p.n_blk - 1 - (L - bhr * p.n_blk);
+  const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
+  const int b = udiv(bh, p.div_h), h = bh - b * p.H;
+  const MaskGeom g = residue_geom(p.mask, r);
+  const int nblk_r = (g.S + 127) / 128;
+  if (blk >= nblk_r) return;  // whole workgroup, before any barrier
+  const int hkv = udiv(h, p.div_g);
+  const int dil = p.mask.dil;
+  const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
+  const uint16_t* doh = p.dout + b * p.do_sb + h * p.do_sh + r * p.do_ss;
+  const uint16_t* kh = p.k + b * p.k_sb + hkv * p.k_sh + r * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hkv * p.v_sh + r * p.v_ss;
+  uint16_t* dqh = p.dq + b * p.dq_sb + h * p.dq_sh + r * p.dq_ss;
+  const int64_t qrs = p.q_ss * dil, dors = p.do_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil,
+                dqrs = p.dq_ss * dil;
+  ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
+  sg.c1 = p.scale * (p.head_scale ? p.head_scale[h] : 1.0f);
+  sg.sl = (ALIBI && p.alibi_slopes) ? p.alibi_slopes[h] * (float)dil : 0.0f;
+
+  // this wavefront's 32 rows: Q and dO as MFMA B operands (lane = row)
+  const int row0 = blk * 128 + 32 * wave;
+  const int i = row0 + lq;
+  const bool ok = i < g.S;
+  bf16x8_t qf[DK], df[DK];
+  {
+    const uint16_t* qs = qh + (int64_t)(ok ? i : 0) * qrs + 8 * lh;
+    const uint16_t* ds = doh + (int64_t)(ok ? i : 0) * dors + 8 * lh;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      qf[kk] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qs + 16 * kk));
+      df[kk] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(ds + 16 * kk));
+    }
+  }
+  float lse2 = 0.f, delta = 0.f;
+  if constexpr (NORM == NORM_SOFTMAX) {
+    const int64_t o2 = ((int64_t)bh * p.residues + r) * p.SR + (ok ? i : 0);
+    lse2 = p.stats[o2];
+    delta = p.stats[(int64_t)p.B * p.H * p.residues * p.SR + o2];
+  }
+
+  // key tiles of the workgroup's rows; per-wavefront classification bounds
+  const int wg_hi = imin32(blk * 128 + 127, g.S - 1);
+  const TileRange tr = tile_range(g, blk * 128, wg_hi, BN);
+  const int ntiles = tr.n_pre + tr.n2;
+  const bool wvalid = row0 < g.S;
+  const int ra = row0, rb = imin32(row0 + 31, g.S - 1);
+
+  f32x16_t dq[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dq[db][e] = 0.f;
+
+  // LDS lane offsets: row reads (A = K or V rows) and transposed reads (A = K^T)
+  const int k_lane = lq * RP + 16 * k_slot(lq, lh);
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int t_row = 4 * (g16 >> 1) + (s16 >> 2);
+  const int t_lane = t_row * RP + 16 * ((2 * (g16 & 1) + ((s16 & 3) >> 1)) ^ t_row) + 8 * (s16 & 1);
+
+  auto issue = [&](int it) {
+    const int jt0 = tile_at(tr, it) * BN;
+    char* st = lds + (it % NS) * STAGE_BYTES;
+    dma_rows<D, NW>(kh, krs, jt0, g.S, st, wave, lane);
+    dma_rows<D, NW>(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
+  };
+  constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64));  // loads per tile per wavefront
+  int dma_next = 0;
+  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+
+  typedef short i16x8_t __attribute__((ext_vector_type(8)));
+  for (int it = 0; it < ntiles; ++it) {
+    if (dma_next - (it + 1) >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA2) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (dma_next < ntiles) issue(dma_next++);
+    const char* St = lds + (it % NS) * STAGE_BYTES;
+    const int jt0 = tile_at(tr, it) * BN;
+    const int cls = wvalid ? classify_tile(g, ra, rb, jt0, jt0 + BN - 1) : (int)TILE_EMPTY;
+    if (cls == TILE_EMPTY) continue;
+
+    uint32_t pk[KB][8];  // dS^T, bf16 pairs
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      f32x16_t sacc, pacc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < DK; ++kk) {
+        const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
+        const bf16x8_t av = *(const bf16x8_t*)(St + T_BYTES + 32 * kb * RP + (k_lane ^ (32 * kk)));
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], sacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[kk], pacc, 0, 0, 0);
+      }
+      const int jbase = jt0 + 32 * kb + 4 * lh;
+      const uint32_t hidden = cls == TILE_PARTIAL ? hidden_bits(g, i, jbase) : 0u;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        float ds[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const int e = 2 * w + x;
+          const int rc = 8 * (e >> 2) + (e & 3);
+          float pv, dsv;
+          sg(sacc[e], pacc[e], (float)(jbase + rc - i), lse2, delta, pv, dsv);
+          ds[x] = ((hidden >> rc) & 1u) ? 0.f : dsv;
+        }
+        pk[kb][w] = pack_bf16x2(ds[0], ds[1]);
+      }
+    }
+    // dQ^T += K^T dS^T, 16-key chunk by chunk
+#pragma unroll
+    for (int c = 0; c < 2 * KB; ++c) {
+      const int kb = c >> 1, half = c & 1;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const char* ka = St + 16 * c * RP + (t_lane ^ (64 * db));
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)ka);
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(ka + 8 * RP));
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        const u32x4_t wv = {pk[kb][4 * half], pk[kb][4 * half + 1], pk[kb][4 * half + 2], pk[kb][4 * half + 3]};
+        dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8_t, wv), dq[db], 0, 0, 0);
+      }
+    }
+  }
+
+  if (ok) {
+    uint16_t* dst = dqh + (int64_t)i * dqrs + 4 * lh;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2_t w;
+        w[0] = pack_bf16x2(dq[db][4 * gq + 0], dq[db][4 * gq + 1]);
+        w[1] = pack_bf16x2(dq[db][4 * gq + 2], dq[db][4 * gq + 3]);
+        *(u32x2_t*)(dst + 32 * db + 8 * gq) = w;
+      }
+  }
+}
+
+// ---- dK, dV ----------------------------------------------------------------------
+template <int D, int NORM, bool ALIBI, bool SOFTCAP>
+__global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(const BwdParams p) {
+  constexpr int NW = 4, BM = 64, QB = BM / 32, DK = D / 16, DB = D / 32;
+  constexpr int RP = 2 * D, T_BYTES = BM * RP;
+  // stage: Q tile, dO tile, then (softmax) the 64 rows' lse log2 e and delta
+  constexpr bool kStats = NORM == NORM_SOFTMAX;
+  constexpr int STAGE_BYTES = 2 * T_BYTES + (kStats ? 512 : 0);
+  constexpr int NS = 3;
+  constexpr int kMaxGroup = 256;  // query heads per K/V head staged in LDS
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
+  __shared__ float head_c[2 * kMaxGroup];  // per query head of the group: c1, ALiBi slope
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, lh = lane >> 5;
+
+  // workgroup -> (b, K/V head, residue, 128-key block); low blocks (seen by
+  // the most rows under a causal mask) first
+  const int HK = p.H / p.G;
+  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  const int bhr = udiv(L, p.div_blk);
+  const int blk = L - bhr * p.n_blk;
+  const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
+  const int b = udiv(bh, p.div_hk), hkv = bh - b * HK;
+  const MaskGeom g = residue_geom(p.mask, r);
+  const int nblk_r = (g.S + 127) / 128;
+  if (blk >= nblk_r) return;  // whole workgroup, before any barrier
+  const int dil = p.mask.dil;
+  const uint16_t* kh = p.k + b * p.k_sb + hkv * p.k_sh + r * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hkv * p.v_sh + r * p.v_ss;
+  uint16_t* dkh = p.dk + b * p.dk_sb + hkv * p.dk_sh + r * p.dk_ss;
+  uint16_t* dvh = p.dv + b * p.dv_sb + hkv * p.dv_sh + r * p.dv_ss;
+  const int64_t qrs = p.q_ss * dil, dors = p.do_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil,
+                dkrs = p.dk_ss * dil, dvrs = p.dv_ss * dil;
+
+  // the group's per-head score constants, once, before any DMA is in flight
+  for (int t = tid; t < p.G; t += NW * 64) {
+    const int hq = hkv * p.G + t;
+    head_c[t] = p.scale * (p.head_scale ? p.head_scale[hq] : 1.0f);
+    head_c[kMaxGroup + t] = (ALIBI && p.alibi_slopes) ? p.alibi_slopes[hq] * (float)p.mask.dil : 0.0f;
+  }
+  __syncthreads();
+
+  // this wavefront's 32 keys: K and V as MFMA B operands (lane = key)
+  const int key0 = blk * 128 + 32 * wave;
+  const int j = key0 + lq;
+  const bool okj = j < g.S;
+  bf16x8_t kf[DK], vf[DK];
+  {
+    const uint16_t* ks = kh + (int64_t)(okj ? j : 0) * krs + 8 * lh;
+    const uint16_t* vs = vh + (int64_t)(okj ? j : 0) * vrs + 8 * lh;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) {
+      kf[kk] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(ks + 16 * kk));
+      vf[kk] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(vs + 16 * kk));
+    }
+  }
+
+  // query tiles of the rows that see the workgroup's keys, for each query head of the group
+  const RowSpan qs = query_range(g, blk * 128, imin32(blk * 128 + 127, g.S - 1));
+  const int t_lo = qs.lo / BM, n_qt = qs.lo <= qs.hi ? qs.hi / BM - t_lo + 1 : 0;
+  const int ntiles = n_qt * p.G;
+  const bool wvalid = key0 < g.S;
+  const int kc = key0, kd = key0 + 31;
+  // the rows that see this lane's key: an interval (exact for one key; empty
+  // past the end), so a block's per-element mask is one bitmask per lane
+  const RowSpan seen = query_range(g, j, j);
+  const int64_t plane = (int64_t)p.B * p.H * p.residues * p.SR;
+
+  f32x16_t dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) dk[db][e] = dv[db][e] = 0.f;
+
+  const int k_lane = lq * RP + 16 * k_slot(lq, lh);
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int t_row = 4 * (g16 >> 1) + (s16 >> 2);
+  const int t_lane = t_row * RP + 16 * ((2 * (g16 & 1) + ((s16 & 3) >> 1)) ^ t_row) + 8 * (s16 & 1);
+
+  auto tile_head = [&](int it) { return hkv * p.G + it / imax32(n_qt, 1); };
+  auto tile_row = [&](int it) { return (t_lo + it % imax32(n_qt, 1)) * BM; };
+  auto issue = [&](int it) {
+    const int hq = tile_head(it), i0 = tile_row(it);
+    char* st = lds + (it % NS) * STAGE_BYTES;
+    dma_rows<D, NW>(p.q + b * p.q_sb + hq * p.q_sh + r * p.q_ss, qrs, i0, g.S, st, wave, lane);
+    dma_rows<D, NW>(p.dout + b * p.do_sb + hq * p.do_sh + r * p.do_ss, dors, i0, g.S, st + T_BYTES, wave, lane);
+    if constexpr (kStats) {
+      // wavefront w moves 32 floats: lse log2 e rows [32 w, +32) (w < 2), or
+      // delta rows [32 (w - 2), +32); the stats rows are padded to 64
+      const float* src = p.stats + (wave >= 2 ? plane : 0) + ((int64_t)(b * p.H + hq) * p.residues + r) * p.SR + i0 +
+                         32 * (wave & 1);
+      if (lane < 32) dma4s(src, (uint32_t)(4 * lane), lds_addr(st + 2 * T_BYTES + 128 * wave));
+    }
+  };
+  constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64)) + (kStats ? 1 : 0);
+  int dma_next = 0;
+  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+
+  typedef short i16x8_t __attribute__((ext_vector_type(8)));
+  for (int it = 0; it < ntiles; ++it) {
+    if (dma_next - (it + 1) >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA2) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (dma_next < ntiles) issue(dma_next++);
+    const char* St = lds + (it % NS) * STAGE_BYTES;
+    const int hq = tile_head(it), i0 = tile_row(it);
+    // rows past the end of the sub-sequence are clamped copies: mask them
+    int cls = wvalid ? classify_tile(g, i0, imin32(i0 + BM - 1, g.S - 1), kc, kd) : (int)TILE_EMPTY;
+    if (cls == TILE_EMPTY) continue;
+    if (i0 + BM > g.S) cls = TILE_PARTIAL;
+    ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
+    sg.c1 = head_c[hq - hkv * p.G];
+    sg.sl = head_c[kMaxGroup + hq - hkv * p.G];
+    const float* st_stats = (const float*)(St + 2 * T_BYTES);  // [64] lse log2 e, then [64] delta
+
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      f32x16_t sacc, pacc;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < DK; ++kk) {
+        const bf16x8_t a = *(const bf16x8_t*)(St + 32 * qb * RP + (k_lane ^ (32 * kk)));
+        const bf16x8_t ad = *(const bf16x8_t*)(St + T_BYTES + 32 * qb * RP + (k_lane ^ (32 * kk)));
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[kk], sacc, 0, 0, 0);
+        pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[kk], pacc, 0, 0, 0);
+      }
+      // rows of register e: ibase + 8 (e >> 2) + (e & 3)
+      const int ibase = i0 + 32 * qb + 4 * lh;
+      f32x4_t l4[4], d4[4];
+      if constexpr (kStats) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          l4[gq] = *(const f32x4_t*)(st_stats + 32 * qb + 4 * lh + 8 * gq);
+          d4[gq] = *(const f32x4_t*)(st_stats + 64 + 32 * qb + 4 * lh + 8 * gq);
+        }
+      }
+      // bit k: row ibase + k does not see key j
+      const uint32_t hidden = cls == TILE_PARTIAL ? ~key_bits(seen.lo - ibase, seen.hi - ibase) : 0u;
+      uint32_t pp[8], pd[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        float pv[2], dsv[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+          const int e = 2 * w + x;
+          const int rc = 8 * (e >> 2) + (e & 3);
+          const float ls = NORM == NORM_SOFTMAX ? l4[e >> 2][e & 3] : 0.f;
+          const float dl = NORM == NORM_SOFTMAX ? d4[e >> 2][e & 3] : 0.f;
+          sg(sacc[e], pacc[e], (float)(j - (ibase + rc)), ls, dl, pv[x], dsv[x]);
+          const bool hide = (hidden >> rc) & 1u;
+          pv[x] = hide ? 0.f : pv[x];
+          dsv[x] = hide ? 0.f : dsv[x];
+        }
+        pp[w] = pack_bf16x2(pv[0], pv[1]);
+        pd[w] = pack_bf16x2(dsv[0], dsv[1]);
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS, 16-row chunk by chunk
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int c = 2 * qb + half;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const char* qa = St + 16 * c * RP + (t_lane ^ (64 * db));
+          const char* da = St + T_BYTES + 16 * c * RP + (t_lane ^ (64 * db));
+          const i16x4_t qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)qa);
+          const i16x4_t qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(qa + 8 * RP));
+          const i16x4_t dlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)da);
+          const i16x4_t dhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(da + 8 * RP));
+          const bf16x8_t aq = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7));
+          const bf16x8_t ado = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7));
+          const u32x4_t wp = {pp[4 * half], pp[4 * half + 1], pp[4 * half + 2], pp[4 * half + 3]};
+          const u32x4_t wd = {pd[4 * half], pd[4 * half + 1], pd[4 * half + 2], pd[4 * half + 3]};
+          dv[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ado, __builtin_bit_cast(bf16x8_t, wp), dv[db], 0, 0, 0);
+          dk[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aq, __builtin_bit_cast(bf16x8_t, wd), dk[db], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  if (okj) {
+    uint16_t* kdst = dkh + (int64_t)j * dkrs + 4 * lh;
+    uint16_t* vdst = dvh + (int64_t)j * dvrs + 4 * lh;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2_t wk, wv;
+        wk[0] = pack_bf16x2(dk[db][4 * gq + 0], dk[db][4 * gq + 1]);
+        wk[1] = pack_bf16x2(dk[db][4 * gq + 2], dk[db][4 * gq + 3]);
+        wv[0] = pack_bf16x2(dv[db][4 * gq + 0], dv[db][4 * gq + 1]);
+        wv[1] = pack_bf16x2(dv[db][4 * gq + 2], dv[db][4 * gq + 3]);
+        *(u32x2_t*)(kdst + 32 * db + 8 * gq) = wk;
+        *(u32x2_t*)(vdst + 32 * db + 8 * gq) = wv;
+      }
+  }
+}
+
+}  // namespace chia

@@ -72,6 +72,7 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 enum Norm : int { NORM_SOFTMAX = 0, NORM_SIGMOID = 1, NORM_RELU = 2 };
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr int kBN = 64;
 
@@ -94,6 +95,7 @@ struct FwdParams {
   int32_t n_wg;
   UDiv div_pairs, div_res, div_h;  // dividers by n_pairs, residues, H
   UDiv div_group;                  // by query heads per K/V head (GQA / MQA)
+  float* lse;                      // softmax: fp32 [B, H, S] log-sum-exp of the scores, or nullptr
   float scale, softcap, bias, post_scale;
 };
 
@@ -927,6 +929,13 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     if constexpr (NORM == NORM_SOFTMAX) {
       const float lt = xhalf_sum(l_run[qb]);
       f = lt > 0.f ? 1.0f / lt : 0.f;
+      // log-sum-exp of the row's (modified) scores, natural log: the weights
+      // summed into l are 2^(t log2 e - m), so LSE = (m + log2 l) ln 2
+      // (-inf for a row that sees no key)
+      if (p.lse != nullptr && lh == 0 && valid[qb] && i < g.S) {
+        const float lse2 = lt > 0.f ? m_run[qb] + __builtin_amdgcn_logf(lt) : -INFINITY;
+        p.lse[((int64_t)b * p.H + h) * p.mask.S + g.r + (int64_t)g.dil * i] = lse2 * kLn2;
+      }
     } else {
       f = post;
     }

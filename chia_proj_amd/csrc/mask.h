@@ -183,6 +183,34 @@ CHIA_HD TileSpan wide_range_all(const MaskGeom& g, int32_t r0, int32_t r1, bool 
   return s;
 }
 
+// Queries (sub-sequence rows) that may see a key of [j0, j1]: every row when
+// the block holds a prefix key, else the rows whose interval reaches j0
+// (key_hi non-decreasing: a suffix) and starts by j1 (key_lo non-decreasing:
+// a prefix).  A superset of the rows that see the block: rows inside whose
+// interval misses it are classified EMPTY or masked.  Empty when lo > hi.
+struct RowSpan {
+  int32_t lo, hi;
+};
+
+CHIA_HD RowSpan query_range(const MaskGeom& g, int32_t j0, int32_t j1) {
+  if (j0 < g.prefix) return RowSpan{0, g.S - 1};
+  int32_t lo = 0, hi = g.S;  // first row with key_hi >= j0
+  while (lo < hi) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (key_hi(g, mid) >= j0) hi = mid;
+    else lo = mid + 1;
+  }
+  const int32_t first = lo;
+  lo = 0;
+  hi = g.S;  // first row with key_lo > j1
+  while (lo < hi) {
+    const int32_t mid = (lo + hi) >> 1;
+    if (key_lo(g, mid) > j1) hi = mid;
+    else lo = mid + 1;
+  }
+  return RowSpan{first, lo - 1};
+}
+
 // KV tiles of width bn that queries [a, b] may touch: [0, n_pre) followed by
 // [start2, start2 + n2).
 struct TileRange {

@@ -56,7 +56,8 @@ enum chia_attn_status {
   CHIA_ATTN_ERR_SCALE = -5,         /* scale <= 0, non-finite, softcap < 0  */
   CHIA_ATTN_ERR_NORM = -6,          /* unknown normaliser                   */
   CHIA_ATTN_ERR_ALIGN = -7,         /* pointer/stride not 16-byte aligned   */
-  CHIA_ATTN_ERR_STRUCT = -8         /* struct_size does not match this ABI  */
+  CHIA_ATTN_ERR_STRUCT = -8,        /* struct_size does not match this ABI  */
+  CHIA_ATTN_ERR_WORKSPACE = -9      /* backward workspace NULL or too small */
 };
 
 typedef struct chia_attn_args {
@@ -111,6 +112,48 @@ typedef struct chia_attn_args {
  * launch_kernel(q, k, v) of kernels_gemini31propre_0018/<op>_BEST.py
  * (e.g. bias_sliding_window_BEST.py:87-108). */
 int chia_attn_fwd(const chia_attn_args* args, void* stream);
+
+/* chia_attn_fwd that also writes, for a SOFTMAX normaliser, the log-sum-exp of
+ * each row's modified, masked scores: lse[(b * H + h) * S + i] =
+ * log(sum_j visible exp(s_ij)), fp32, -inf for a row that sees no key -- the
+ * statistic chia_attn_bwd needs.  lse must be non-NULL (4-byte aligned) for
+ * SOFTMAX and is ignored for SIGMOID / RELU.  No counterpart in the reference,
+ * whose kernels are forward-only (README.md:223); this is the training
+ * extension's forward. */
+int chia_attn_fwd_lse(const chia_attn_args* args, float* lse, void* stream);
+
+/* Backward of the forward `fwd` describes: given o, lse (SOFTMAX) and
+ * dout = dL/do, writes dq = dL/dq [B, H, S, D] and dk, dv = dL/dk, dL/dv
+ * [B, H_kv, S, D] (bf16; with kv_heads < heads, each K/V head's gradient is
+ * the sum over its query heads).  head_scale and alibi_slopes are constants
+ * (no gradient).  The gradients are those of the exact (unrounded) forward
+ * with the probabilities recomputed from lse.  No counterpart in the
+ * reference (forward-only, README.md:223). */
+typedef struct chia_attn_bwd_args {
+  uint32_t struct_size;       /* sizeof(chia_attn_bwd_args) */
+  uint32_t reserved0;         /* must be zero */
+  const chia_attn_args* fwd;  /* the forward's arguments: q, k, v, o and every parameter */
+  const void* dout;           /* bf16 [B, H, S, D] */
+  void* dq;                   /* bf16 [B, H, S, D], written */
+  void* dk;                   /* bf16 [B, H_kv, S, D], written */
+  void* dv;                   /* bf16 [B, H_kv, S, D], written */
+  int64_t dout_stride[3];     /* batch, head, seq strides in elements */
+  int64_t dq_stride[3];
+  int64_t dk_stride[3];
+  int64_t dv_stride[3];
+  const float* lse;           /* SOFTMAX: [B, H, S] from chia_attn_fwd_lse; else ignored */
+  void* workspace;            /* device memory of chia_attn_bwd_workspace_size bytes */
+  int64_t workspace_bytes;
+  int32_t reserved[8];        /* must be zero */
+} chia_attn_bwd_args;
+
+/* Bytes of workspace chia_attn_bwd needs for `fwd` (fp32 row statistics for
+ * SOFTMAX, 0 otherwise); negative: an argument error. */
+int64_t chia_attn_bwd_workspace_size(const chia_attn_args* fwd);
+
+/* Launch the backward on `stream` (asynchronous; the caller keeps every
+ * buffer alive until it completes).  Status codes as chia_attn_fwd. */
+int chia_attn_bwd(const chia_attn_bwd_args* args, void* stream);
 
 /* Host-only schedule statistics for `args` (no GPU call).  Used by the
  * benchmark's FLOP accounting; the reference has no counterpart (its timer,

@@ -62,8 +62,8 @@ def _mk(q, k, v, *, mod: Optional[Callable] = None, maskfn: Optional[Callable] =
     """mk() of extra_bench.py:37-46 on the CPU; fp32/fp64 unless eager."""
     B, H, S, D = q.shape
     SC = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    if eager:
-        q, k, v = (t.detach().cpu().to(torch.bfloat16) for t in (q, k, v))
+    if eager:  # differentiable (torch autograd of the eager bf16 path is a calibration point for gradients)
+        q, k, v = (t.cpu().to(torch.bfloat16) for t in (q, k, v))
     else:
         q, k, v = (t.detach().cpu().to(dtype) for t in (q, k, v))
     s = (q @ k.transpose(-2, -1)) * SC

@@ -41,10 +41,56 @@ static int check_hidden_bits(long* n) {
   return 0;
 }
 
+// query_range against visible(): every row that sees a key of the block lies
+// inside the returned span (key blocks of 32 and 64 keys)
+static int check_query_range(long* n) {
+  for (int S : {1, 37, 65, 200, 513})
+    for (int causal = 0; causal < 2; ++causal)
+      for (int w : {0, 1, 5, 64, 129})
+        for (int d : {1, 2, 3})
+          for (int blk : {0, 33, 128})
+            for (int pre : {0, 40, 130}) {
+              if (d > 1 && pre > 0) continue;
+              const MaskSpec m = make_mask_spec(S, causal, w, d, blk, pre);
+              for (int r = 0; r < num_residues(m); ++r) {
+                const MaskGeom g = residue_geom(m, r);
+                // one key: the span is exact (the backward's per-key row mask);
+                // keys past the end give an empty span
+                for (int j = 0; j < g.S + 40; ++j) {
+                  const RowSpan q = query_range(g, j, j);
+                  for (int i = 0; i < g.S; ++i) {
+                    ++*n;
+                    if ((i >= q.lo && i <= q.hi) != visible(g, i, j)) {
+                      std::printf("single-key query_range not exact S=%d c=%d w=%d d=%d blk=%d p=%d r=%d i=%d j=%d\n", S,
+                                  causal, w, d, blk, pre, r, i, j);
+                      return 1;
+                    }
+                  }
+                }
+                for (int bk : {32, 64})
+                  for (int j0 = 0; j0 < g.S; j0 += bk) {
+                    const RowSpan q = query_range(g, j0, j0 + bk - 1);
+                    for (int i = 0; i < g.S; ++i) {
+                      bool sees = false;
+                      for (int j = j0; j < j0 + bk && j < g.S; ++j) sees = sees || visible(g, i, j);
+                      ++*n;
+                      if (sees && (i < q.lo || i > q.hi)) {
+                        std::printf("query_range misses S=%d c=%d w=%d d=%d blk=%d p=%d r=%d j0=%d i=%d span=[%d,%d]\n", S,
+                                    causal, w, d, blk, pre, r, j0, i, q.lo, q.hi);
+                        return 1;
+                      }
+                    }
+                  }
+              }
+            }
+  return 0;
+}
+
 int main() {
   const int bn = 64;
-  long n_bits = 0;
+  long n_bits = 0, n_rows = 0;
   if (check_hidden_bits(&n_bits)) return 1;
+  if (check_query_range(&n_rows)) return 1;
   long checked = 0, fast = 0, wide_all = 0;
   const int seqs[] = {1, 63, 64, 65, 200, 511, 700, 1024};
   const int windows[] = {0, 1, 5, 64, 129, 300};
@@ -126,7 +172,7 @@ int main() {
                 }
               }
             }
-  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span, %ld mask bits\n", checked, fast,
-              wide_all, n_bits);
+  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span, %ld mask bits, %ld query-range rows\n",
+              checked, fast, wide_all, n_bits, n_rows);
   return 0;
 }

@@ -42,7 +42,8 @@ def _c_struct_fields(text, name):
     return fields
 
 
-@pytest.mark.parametrize("cname,pyclass", [("chia_attn_args", _lib.AttnArgs), ("chia_attn_plan_info", _lib.PlanInfo)])
+@pytest.mark.parametrize("cname,pyclass", [("chia_attn_args", _lib.AttnArgs), ("chia_attn_plan_info", _lib.PlanInfo),
+                                           ("chia_attn_bwd_args", _lib.BwdArgs)])
 def test_ctypes_mirrors_header_struct(cname, pyclass):
     fields = _c_struct_fields(HEADER.read_text(), cname)
     assert fields == [f[0] for f in pyclass._fields_]
@@ -50,7 +51,7 @@ def test_ctypes_mirrors_header_struct(cname, pyclass):
 
 def test_status_strings_and_version(lib_built):
     assert lib_built.chia_attn_abi_version() == _lib.ABI_VERSION
-    for st in (0, -1, -2, -3, -4, -5, -6, -7, -8):
+    for st in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
         assert _lib.status_string(st)
     assert "unknown" in _lib.status_string(-99)
 
@@ -170,3 +171,57 @@ def test_plan_geometry(lib_built):
         p = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=64, **kw))
         assert p["wave_tiles_visited"] * 32 * 64 >= p["pairs_visible"]
         assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]
+
+
+def _bwd_ready_args(norm="softmax", **kw):
+    """Forward args with fake (aligned, never dereferenced) device pointers."""
+    a = make_args(batch=1, heads=4, seqlen=128, head_dim=64, norm=norm)
+    a.q = a.k = a.v = a.o = 0x10000
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = 4 * 128 * 64, 128 * 64, 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _bwd_status(a, **kw):
+    b = _lib.BwdArgs(fwd=ctypes.pointer(a), dout=0x20000, dq=0x30000, dk=0x40000, dv=0x50000, lse=0x60000,
+                     workspace=0x70000, workspace_bytes=1 << 30)
+    for name in ("dout_stride", "dq_stride", "dk_stride", "dv_stride"):
+        st = getattr(b, name)
+        st[0], st[1], st[2] = 4 * 128 * 64, 128 * 64, 64
+    for k, v in kw.items():
+        setattr(b, k, v)
+    return _lib.lib().chia_attn_bwd(ctypes.byref(b), None)
+
+
+def test_bwd_workspace_size(lib_built):
+    # softmax: lse log2 e and delta per (b, h, residue, row padded to 64 rows), fp32
+    a = make_args(batch=2, heads=3, seqlen=100, head_dim=64)
+    assert lib_built.chia_attn_bwd_workspace_size(ctypes.byref(a)) == 2 * 2 * 3 * 128 * 4
+    a = make_args(batch=2, heads=3, seqlen=100, head_dim=64, dilation=3)  # residues of 34, 33, 33 rows
+    assert lib_built.chia_attn_bwd_workspace_size(ctypes.byref(a)) == 2 * 2 * 3 * 3 * 64 * 4
+    for norm in ("sigmoid", "relu"):
+        a = make_args(batch=2, heads=3, seqlen=100, head_dim=64, norm=norm)
+        assert lib_built.chia_attn_bwd_workspace_size(ctypes.byref(a)) == 0
+    a = make_args(batch=1, heads=1, seqlen=100, head_dim=96)
+    assert lib_built.chia_attn_bwd_workspace_size(ctypes.byref(a)) == -3
+
+
+def test_bwd_rejects_bad_arguments_without_launching(lib_built):
+    assert lib_built.chia_attn_bwd(None, None) == -1
+    a = _bwd_ready_args()
+    assert _bwd_status(a, struct_size=8) == -8
+    assert _bwd_status(a, reserved0=1) == -8
+    assert _bwd_status(a, dq=None) == -1
+    assert _bwd_status(a, dk=0x40008) == -7          # misaligned
+    assert _bwd_status(a, lse=None) == -1            # softmax needs the forward's lse
+    assert _bwd_status(a, workspace=None) == -9
+    assert _bwd_status(a, workspace_bytes=8) == -9
+    b = _bwd_ready_args(head_dim=96)
+    assert _bwd_status(b) == -3
+    c = _bwd_ready_args(norm="relu")
+    assert _bwd_status(c, lse=None, workspace=None, workspace_bytes=0, dq=None) == -1
+    d = _bwd_ready_args(heads=512, kv_heads=1)       # more than 256 query heads per K/V head
+    assert _bwd_status(d) == -2
