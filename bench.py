@@ -113,6 +113,43 @@ def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16, reps: int = 5):
     }
 
 
+def backward_report(cases, inputs, works, args) -> int:
+    """Per variant: HIP-event median of torch.autograd.grad(o, (q, k, v), do) -- the
+    chia_attn_bwd launches (row statistics, dQ, dK/dV) -- and its algorithmic rate,
+    counting the 5 matmuls of the gradient (10 D per visible pair, 2.5x the forward)."""
+    import torch
+
+    from chia_proj_amd import OPS
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS
+    from chia_proj_amd.timing import median_us
+
+    rows, total_us, total_flops = {}, 0.0, 0.0
+    for c in cases:
+        q, k, v, params = inputs[c.name]
+        qg, kg, vg = (t.detach().requires_grad_(True) for t in (q, k, v))
+        g = torch.Generator("cpu").manual_seed(4242)
+        do = torch.randn(q.shape, generator=g).to(torch.bfloat16).to(q.device)
+        o = OPS[c.op](qg, kg, vg, **params)
+        us = median_us(lambda: torch.autograd.grad(o, (qg, kg, vg), do, retain_graph=True))
+        flops = 2.5 * works[c.name]["flops_alg"]
+        tf = flops / (us * 1e-6) / 1e12
+        rows[c.op] = {"us": round(us, 2), "tflops_alg": round(tf, 2),
+                      "pct_mfma_peak_alg": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
+        total_us += us
+        total_flops += flops
+        log(f"  backward {c.op:22s} {us:9.1f} us  alg {tf:7.1f} TF/s ({100 * tf / PEAK_BF16_TFLOPS:5.1f}% peak)")
+    c0 = cases[0]
+    print(json.dumps({
+        "metric": "backward (dq, dk, dv) us/call + algorithmic TFLOP/s per variant",
+        "value": round(total_flops / (total_us * 1e-6) / 1e12, 2), "unit": "TFLOP/s", "higher_is_better": True,
+        "dtype": "bf16", "data": "synthetic", "n_gpus": 1,
+        "config": {"workload": f"backward of the ten variants, B{c0.B} H{c0.H} S{c0.S} D{c0.D} bf16",
+                   "suite": args.suite},
+        "variants": rows,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,6 +161,9 @@ def main() -> int:
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-calibration", action="store_true")
     ap.add_argument("--report", default="", help="also write the JSON line to this file")
+    ap.add_argument("--backward", action="store_true",
+                    help="time the backward (chia_attn_bwd: dq, dk, dv) of each variant instead of the forward step; "
+                         "prints its own JSON line (not the headline metric)")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
                          "kernel that reads and writes 512 MiB, and exit")
@@ -160,6 +200,8 @@ def main() -> int:
         inputs[c.name] = (q, k, v, params)
         calls[c.name] = (lambda fn=OPS[c.op], q=q, k=k, v=v, p=params: fn(q, k, v, **p))
         works[c.name] = work(c.op, c.B, c.H, c.S, c.D, params)
+    if args.backward:
+        return backward_report(cases, inputs, works, args)
     outputs = {c.name: calls[c.name]() for c in cases}
     torch.cuda.synchronize()
 

@@ -75,49 +75,82 @@ struct BwdParams {
 };
 
 // Per-score gradient (see the header): from the raw s = q.k, dp = do.v and
-// j - i, the probability p (for dV) and ds (for dQ, dK).
+// j - i, the probability p (for dV) and ds / c1 (for dQ, dK: the caller
+// applies c1, once per accumulated gradient where it is uniform).
 template <int NORM, bool ALIBI, bool SOFTCAP>
 struct ScoreGrad {
-  float c1, sl, cap, k2cap, post, nbias_l2;
+  float c1, c1l2, sl, cap, k2cap, post, nbias_l2;
 
   __device__ __forceinline__ void operator()(float s, float dp, float jmi, float lse2, float delta, float& p,
                                              float& ds) const {
-    float u = s * c1;
-    if constexpr (ALIBI) u = __builtin_fmaf(sl, jmi, u);
-    float t = u, dtdu = 1.0f;
-    if constexpr (SOFTCAP) {
-      // tanh(u / cap) = 1 - 2 / (1 + 2^(2 u log2e / cap))
-      const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * k2cap));
-      t = cap * th;
-      dtdu = __builtin_fmaf(-th, th, 1.0f);
-    }
-    float dt;
-    if constexpr (NORM == NORM_SOFTMAX) {
-      p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, kLog2e, -lse2));
-      dt = p * (dp - delta);
-    } else if constexpr (NORM == NORM_SIGMOID) {
-      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(-t, kLog2e, nbias_l2)));
-      p = post * sg;
-      dt = dp * p * (1.0f - sg);
+    if constexpr (!ALIBI && !SOFTCAP) {
+      // t = s c1: the scale folds into one fma ahead of the exponential
+      if constexpr (NORM == NORM_SOFTMAX) {
+        p = __builtin_amdgcn_exp2f(__builtin_fmaf(s, c1l2, -lse2));
+        ds = p * (dp - delta);
+      } else if constexpr (NORM == NORM_SIGMOID) {
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(s, -c1l2, nbias_l2)));
+        p = post * sg;
+        ds = dp * p * (1.0f - sg);
+      } else {
+        const float t = s * c1;
+        p = post * fmaxf(t, 0.0f);
+        ds = t > 0.0f ? dp * post : 0.0f;
+      }
     } else {
-      p = post * fmaxf(t, 0.0f);
-      dt = t > 0.0f ? dp * post : 0.0f;
+      float u = s * c1;
+      if constexpr (ALIBI) u = __builtin_fmaf(sl, jmi, u);
+      float t = u, dtdu = 1.0f;
+      if constexpr (SOFTCAP) {
+        // tanh(u / cap) = 1 - 2 / (1 + 2^(2 u log2e / cap))
+        const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * k2cap));
+        t = cap * th;
+        dtdu = __builtin_fmaf(-th, th, 1.0f);
+      }
+      float dt;
+      if constexpr (NORM == NORM_SOFTMAX) {
+        p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, kLog2e, -lse2));
+        dt = p * (dp - delta);
+      } else if constexpr (NORM == NORM_SIGMOID) {
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(-t, kLog2e, nbias_l2)));
+        p = post * sg;
+        dt = dp * p * (1.0f - sg);
+      } else {
+        p = post * fmaxf(t, 0.0f);
+        dt = t > 0.0f ? dp * post : 0.0f;
+      }
+      ds = dt * dtdu;
     }
-    ds = dt * dtdu * c1;
+  }
+
+  __device__ __forceinline__ void set_head(float c1_, float sl_) {
+    c1 = c1_;
+    c1l2 = c1_ * kLog2e;
+    sl = sl_;
   }
 };
+
+// Zero the elements of x[16] whose bit rc(e) = 8 (e >> 2) + (e & 3) is set in
+// `hidden` (v_bfe_i32 + one bitwise blend per element, no compare / select).
+__device__ __forceinline__ void zero_hidden(float* x, uint32_t hidden) {
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)hidden, 8 * (e >> 2) + (e & 3), 1);
+    asm("" : "+v"(m));  // keeps the and-not bitwise
+    x[e] = __uint_as_float(__float_as_uint(x[e]) & ~m);
+  }
+}
 
 // The per-call constants (no memory access); c1 and sl are the query head's
 // scale * head_scale and ALiBi slope per sub-sequence step, set by the caller.
 template <int NORM, bool ALIBI, bool SOFTCAP>
 __device__ __forceinline__ ScoreGrad<NORM, ALIBI, SOFTCAP> score_consts(const BwdParams& p) {
   ScoreGrad<NORM, ALIBI, SOFTCAP> f;
-  f.c1 = p.scale;
-  f.sl = 0.0f;
   f.cap = p.softcap;
   f.k2cap = SOFTCAP ? 2.0f * kLog2e / p.softcap : 0.0f;
   f.post = p.post_scale;
   f.nbias_l2 = -p.bias * kLog2e;
+  f.set_head(p.scale, 0.0f);
   return f;
 }
 
@@ -208,8 +241,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   const int64_t qrs = p.q_ss * dil, dors = p.do_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil,
                 dqrs = p.dq_ss * dil;
   ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
-  sg.c1 = p.scale * (p.head_scale ? p.head_scale[h] : 1.0f);
-  sg.sl = (ALIBI && p.alibi_slopes) ? p.alibi_slopes[h] * (float)dil : 0.0f;
+  sg.set_head(p.scale * (p.head_scale ? p.head_scale[h] : 1.0f),
+              (ALIBI && p.alibi_slopes) ? p.alibi_slopes[h] * (float)dil : 0.0f);
 
   // this wavefront's 32 rows: Q and dO as MFMA B operands (lane = row)
   const int row0 = blk * 128 + 32 * wave;
@@ -287,20 +320,15 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
         pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, df[kk], pacc, 0, 0, 0);
       }
       const int jbase = jt0 + 32 * kb + 4 * lh;
-      const uint32_t hidden = cls == TILE_PARTIAL ? hidden_bits(g, i, jbase) : 0u;
+      float ds[16];
 #pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        float ds[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const int e = 2 * w + x;
-          const int rc = 8 * (e >> 2) + (e & 3);
-          float pv, dsv;
-          sg(sacc[e], pacc[e], (float)(jbase + rc - i), lse2, delta, pv, dsv);
-          ds[x] = ((hidden >> rc) & 1u) ? 0.f : dsv;
-        }
-        pk[kb][w] = pack_bf16x2(ds[0], ds[1]);
+      for (int e = 0; e < 16; ++e) {
+        float pv;
+        sg(sacc[e], pacc[e], (float)(jbase + 8 * (e >> 2) + (e & 3) - i), lse2, delta, pv, ds[e]);
       }
+      if (cls == TILE_PARTIAL) zero_hidden(ds, hidden_bits(g, i, jbase));
+#pragma unroll
+      for (int w = 0; w < 8; ++w) pk[kb][w] = pack_bf16x2(ds[2 * w], ds[2 * w + 1]);
     }
     // dQ^T += K^T dS^T, 16-key chunk by chunk
 #pragma unroll
@@ -319,14 +347,15 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   }
 
   if (ok) {
+    const float c1 = sg.c1;  // ds was accumulated without the head's scale
     uint16_t* dst = dqh + (int64_t)i * dqrs + 4 * lh;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2_t w;
-        w[0] = pack_bf16x2(dq[db][4 * gq + 0], dq[db][4 * gq + 1]);
-        w[1] = pack_bf16x2(dq[db][4 * gq + 2], dq[db][4 * gq + 3]);
+        w[0] = pack_bf16x2(dq[db][4 * gq + 0] * c1, dq[db][4 * gq + 1] * c1);
+        w[1] = pack_bf16x2(dq[db][4 * gq + 2] * c1, dq[db][4 * gq + 3] * c1);
         *(u32x2_t*)(dst + 32 * db + 8 * gq) = w;
       }
   }
@@ -446,8 +475,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     if (cls == TILE_EMPTY) continue;
     if (i0 + BM > g.S) cls = TILE_PARTIAL;
     ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
-    sg.c1 = head_c[hq - hkv * p.G];
-    sg.sl = head_c[kMaxGroup + hq - hkv * p.G];
+    sg.set_head(head_c[hq - hkv * p.G], head_c[kMaxGroup + hq - hkv * p.G]);
     const float* st_stats = (const float*)(St + 2 * T_BYTES);  // [64] lse log2 e, then [64] delta
 
 #pragma unroll
@@ -472,25 +500,26 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
           d4[gq] = *(const f32x4_t*)(st_stats + 64 + 32 * qb + 4 * lh + 8 * gq);
         }
       }
-      // bit k: row ibase + k does not see key j
-      const uint32_t hidden = cls == TILE_PARTIAL ? ~key_bits(seen.lo - ibase, seen.hi - ibase) : 0u;
+      float pv[16], dsv[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int rc = 8 * (e >> 2) + (e & 3);
+        const float ls = NORM == NORM_SOFTMAX ? l4[e >> 2][e & 3] : 0.f;
+        const float dl = NORM == NORM_SOFTMAX ? d4[e >> 2][e & 3] : 0.f;
+        sg(sacc[e], pacc[e], (float)(j - (ibase + rc)), ls, dl, pv[e], dsv[e]);
+        dsv[e] *= sg.c1;  // the group's query heads may have different scales
+      }
+      if (cls == TILE_PARTIAL) {
+        // bit k: row ibase + k does not see key j
+        const uint32_t hidden = ~key_bits(seen.lo - ibase, seen.hi - ibase);
+        zero_hidden(pv, hidden);
+        zero_hidden(dsv, hidden);
+      }
       uint32_t pp[8], pd[8];
 #pragma unroll
       for (int w = 0; w < 8; ++w) {
-        float pv[2], dsv[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-          const int e = 2 * w + x;
-          const int rc = 8 * (e >> 2) + (e & 3);
-          const float ls = NORM == NORM_SOFTMAX ? l4[e >> 2][e & 3] : 0.f;
-          const float dl = NORM == NORM_SOFTMAX ? d4[e >> 2][e & 3] : 0.f;
-          sg(sacc[e], pacc[e], (float)(j - (ibase + rc)), ls, dl, pv[x], dsv[x]);
-          const bool hide = (hidden >> rc) & 1u;
-          pv[x] = hide ? 0.f : pv[x];
-          dsv[x] = hide ? 0.f : dsv[x];
-        }
-        pp[w] = pack_bf16x2(pv[0], pv[1]);
-        pd[w] = pack_bf16x2(dsv[0], dsv[1]);
+        pp[w] = pack_bf16x2(pv[2 * w], pv[2 * w + 1]);
+        pd[w] = pack_bf16x2(dsv[2 * w], dsv[2 * w + 1]);
       }
       // dV^T += dO^T P, dK^T += Q^T dS, 16-row chunk by chunk
 #pragma unroll
