@@ -130,6 +130,11 @@ def backward_report(cases, inputs, works, args) -> int:
         g = torch.Generator("cpu").manual_seed(4242)
         do = torch.randn(q.shape, generator=g).to(torch.bfloat16).to(q.device)
         o = OPS[c.op](qg, kg, vg, **params)
+        if args.pmc_mode:  # two backward passes per variant for the counters, nothing timed
+            for _ in range(2):
+                torch.autograd.grad(o, (qg, kg, vg), do, retain_graph=True)
+            torch.cuda.synchronize()
+            continue
         us = median_us(lambda: torch.autograd.grad(o, (qg, kg, vg), do, retain_graph=True))
         flops = 2.5 * works[c.name]["flops_alg"]
         tf = flops / (us * 1e-6) / 1e12
@@ -138,6 +143,9 @@ def backward_report(cases, inputs, works, args) -> int:
         total_us += us
         total_flops += flops
         log(f"  backward {c.op:22s} {us:9.1f} us  alg {tf:7.1f} TF/s ({100 * tf / PEAK_BF16_TFLOPS:5.1f}% peak)")
+    if args.pmc_mode:
+        print(json.dumps({"pmc_mode": True, "backward": True, "variants": [c.op for c in cases]}), flush=True)
+        return 0
     c0 = cases[0]
     print(json.dumps({
         "metric": "backward (dq, dk, dv) us/call + algorithmic TFLOP/s per variant",
@@ -166,7 +174,7 @@ def main() -> int:
                          "prints its own JSON line (not the headline metric)")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
-                         "kernel that reads and writes 512 MiB, and exit")
+                         "kernel that reads and writes 512 MiB, and exit (with --backward: two backward passes per variant)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
