@@ -51,8 +51,9 @@ def _head_key(vals: PerHead):
 
 
 def _per_head_vector(vals: PerHead, heads: int, device: torch.device, name: str,
-                     positive: bool) -> Optional[torch.Tensor]:
-    """float32 [heads] device vector for a per-head parameter (cached for host values)."""
+                     positive: bool, cache: bool = True) -> Optional[torch.Tensor]:
+    """float32 [heads] device vector for a per-head parameter (cached for host values
+    unless `cache` is False, as while tracing with fake tensors)."""
     if vals is None:
         return None
     if isinstance(vals, torch.Tensor) and vals.device.type == "cuda":
@@ -62,17 +63,27 @@ def _per_head_vector(vals: PerHead, heads: int, device: torch.device, name: str,
         if t.device != device:
             raise ValueError(f"{name} is on {t.device}, tensors are on {device}")
         return t.to(torch.float32).contiguous()
-    host = torch.as_tensor(vals, dtype=torch.float32).reshape(-1)
-    if host.numel() != heads:
-        raise ValueError(f"{name} must have {heads} values, got {host.numel()}")
-    if not torch.isfinite(host).all():
+    # host values: checked in Python (no tensor op, so fake-tensor tracing can run this)
+    if isinstance(vals, torch.Tensor):
+        if not cache:  # tracing: the values are not read on the host (nor checked)
+            t = vals.detach().to(torch.float32).reshape(-1)
+            if t.numel() != heads:
+                raise ValueError(f"{name} must have {heads} values, got {t.numel()}")
+            return t.to(device)
+        vals = vals.detach().reshape(-1).tolist()
+    host = [float(x) for x in vals]
+    if len(host) != heads:
+        raise ValueError(f"{name} must have {heads} values, got {len(host)}")
+    if not all(math.isfinite(x) for x in host):
         raise ValueError(f"{name} must be finite")
-    if positive and not (host > 0).all():
+    if positive and not all(x > 0 for x in host):
         raise ValueError(f"{name} must be > 0")
-    key = (name, device.index, tuple(host.tolist()))
+    if not cache:
+        return torch.tensor(host, dtype=torch.float32).to(device)  # a host constant, then a copy (traceable)
+    key = (name, device.index, tuple(host))
     cached = _vec_cache.get(key)
     if cached is None:
-        cached = host.to(device)
+        cached = torch.tensor(host, dtype=torch.float32).to(device)
         _vec_cache[key] = cached
         if len(_vec_cache) > _VEC_CACHE_MAX:
             _vec_cache.popitem(last=False)
@@ -134,10 +145,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
     params = dict(norm=norm, causal=causal, window=window, dilation=dilation, block=block, prefix=prefix,
                   scale=scale, head_scale=head_scale, alibi_slopes=alibi_slopes, softcap=softcap, bias=bias,
                   post_scale=post_scale)
-    if torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v)):
+    needs_grad = torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v))
+    if needs_grad or torch.compiler.is_compiling():
+        # the registered operator: autograd (chia_attn::bwd) and torch.compile see one node
         if out is not None:
-            raise ValueError("out= is not supported when q, k or v requires grad")
-        return _AttentionFn.apply(q, k, v, params)
+            raise ValueError("out= is not supported when q, k or v requires grad or under torch.compile")
+        return _op_forward(q, k, v, params)[0]
     # Fast path: a call with the same shapes, layouts and parameters as an
     # earlier one reuses its validated argument struct and per-head vectors;
     # only the data pointers (and their alignment) are new.
@@ -242,43 +255,44 @@ def _strides3(t: torch.Tensor):
     return t.stride(0), t.stride(1), t.stride(2)
 
 
-class _AttentionFn(torch.autograd.Function):
-    """attention() with gradients: the forward also keeps the softmax log-sum-exp
-    (chia_attn_fwd_lse); the backward launches chia_attn_bwd (dq, dk, dv; the
-    per-head vectors, softcap, bias and post_scale are constants)."""
+def _op_forward(q, k, v, params):
+    """(o, lse) through torch.ops.chia_attn.fwd, per-head values as float32 device vectors."""
+    from .library import call_fwd
 
-    @staticmethod
-    def forward(ctx, q, k, v, params):
-        a, hs, sl, (q_, k_, v_), o = _prepare(q, k, v, None, **params)
-        B, H, S, _ = q_.shape
-        lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device) if params["norm"] == "softmax" else None
-        with torch.cuda.device(q.device):
-            stream = torch.cuda.current_stream(q.device).cuda_stream
-            _lib.fwd_lse(a, lse.data_ptr() if lse is not None else 0, stream)
-        ctx.params = params
-        ctx.vecs = (hs, sl)  # the device vectors the argument struct points at
-        ctx.save_for_backward(q_, k_, v_, o, *(() if lse is None else (lse,)))
-        return o
+    if not isinstance(q, torch.Tensor) or q.dim() != 4:
+        raise ValueError("q must be a 4-D [B, H, S, D] tensor")
+    p = dict(params)
+    H = q.shape[1]
+    # no cached device vectors while tracing (fake tensors, torch.compile)
+    cache = (q.device.type == "cuda" and not torch.compiler.is_compiling()
+             and not isinstance(q, torch._subclasses.fake_tensor.FakeTensor))
+    p["head_scale"] = _per_head_vector(p["head_scale"], H, q.device, "head_scale", positive=True, cache=cache)
+    p["alibi_slopes"] = _per_head_vector(p["alibi_slopes"], H, q.device, "alibi_slopes", positive=False,
+                                         cache=cache)
+    return call_fwd(q, k, v, p)
 
-    @staticmethod
-    def backward(ctx, do):
-        q_, k_, v_, o, *rest = ctx.saved_tensors
-        lse = rest[0] if rest else None
-        a, _, _, _, _ = _prepare(q_, k_, v_, o, **ctx.params)
-        do_ = do if (do.dtype == torch.bfloat16 and _layout_ok(do)) else do.to(torch.bfloat16).contiguous()
-        dq, dk, dv = torch.empty_like(q_), torch.empty_like(k_), torch.empty_like(v_)
-        nbytes = _lib.bwd_workspace_size(a)
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q_.device)
-        b = _lib.BwdArgs(dout=do_.data_ptr(), dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
-                         lse=lse.data_ptr() if lse is not None else None, workspace=ws.data_ptr(),
-                         workspace_bytes=nbytes)
-        b.fwd = ctypes.pointer(a)
-        for name, t in (("dout_stride", do_), ("dq_stride", dq), ("dk_stride", dk), ("dv_stride", dv)):
-            st = getattr(b, name)
-            st[0], st[1], st[2] = _strides3(t)
-        with torch.cuda.device(q_.device):
-            _lib.bwd(b, torch.cuda.current_stream(q_.device).cuda_stream)
-        return dq, dk, dv, None
+
+def run_backward(do, q, k, v, o, lse, params):
+    """dq, dk, dv by chia_attn_bwd (lse: the forward's float32 [B, H, S], softmax only)."""
+    a, _, _, (q_, k_, v_), _ = _prepare(q, k, v, o, **params)
+    do_ = do if (do.dtype == torch.bfloat16 and _layout_ok(do)) else do.to(torch.bfloat16).contiguous()
+    if do_.shape != q.shape:
+        raise ValueError(f"do must have q's shape {tuple(q.shape)}, got {tuple(do.shape)}")
+    if (lse is None) != (params["norm"] != "softmax"):
+        raise ValueError("lse is required for softmax and unused otherwise")
+    dq, dk, dv = (torch.empty(t.shape, dtype=torch.bfloat16, device=t.device) for t in (q_, k_, v_))
+    nbytes = _lib.bwd_workspace_size(a)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q_.device)
+    b = _lib.BwdArgs(dout=do_.data_ptr(), dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
+                     lse=lse.data_ptr() if lse is not None else None, workspace=ws.data_ptr(),
+                     workspace_bytes=nbytes)
+    b.fwd = ctypes.pointer(a)
+    for name, t in (("dout_stride", do_), ("dq_stride", dq), ("dk_stride", dk), ("dv_stride", dv)):
+        st = getattr(b, name)
+        st[0], st[1], st[2] = _strides3(t)
+    with torch.cuda.device(q_.device):
+        _lib.bwd(b, torch.cuda.current_stream(q_.device).cuda_stream)
+    return dq, dk, dv
 
 
 def plan(*, batch: int, heads: int, seqlen: int, head_dim: int, **mask_kw) -> dict:

@@ -1,0 +1,117 @@
+"""torch.library registration of the attention core: ``chia_attn::fwd`` and ``chia_attn::bwd``.
+
+The reference's kernels are plain Python functions that launch on torch's
+current stream (extra_bench.py:12,19); torch.compile traces into them and
+breaks its graph at the launch.  Registered as custom operators with fake
+(shape-only) implementations and an autograd formula, the core is one opaque
+node to torch.compile, make_fx and AOTAutograd -- the "operators Inductor does
+not cover" use of the reference's README.md:3-6 -- and gradients flow through
+the registered backward.
+
+  chia_attn::fwd(q, k, v, <mask and score parameters>) -> (o, lse)
+      o: bf16 like q; lse: float32 [B, H, S] (natural log, softmax only; an
+      empty [0] tensor for sigmoid / ReLU).  lse is not differentiable.
+  chia_attn::bwd(do, q, k, v, o, lse, <parameters>) -> (dq, dk, dv)
+
+Per-head vectors are optional float32 device tensors [H]; ``scale`` None
+stands for the default 1 / sqrt(head_dim).  Both operators run
+``chia_attn_fwd_lse`` / ``chia_attn_bwd`` of libchia_attn.so on torch's current
+stream, and raise if the library is not built.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+NAMESPACE = "chia_attn"
+
+
+def _params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap, bias,
+            post_scale) -> dict:
+    return dict(norm=norm, causal=causal, window=window, dilation=dilation, block=block, prefix=prefix,
+                scale=scale, head_scale=head_scale, alibi_slopes=alibi_slopes,
+                softcap=softcap, bias=bias, post_scale=post_scale)
+
+
+@torch.library.custom_op(f"{NAMESPACE}::fwd", mutates_args=(), device_types="cuda")
+def fwd(q: Tensor, k: Tensor, v: Tensor, norm: str, causal: bool, window: int, dilation: int, block: int,
+        prefix: int, scale: Optional[float], head_scale: Optional[Tensor], alibi_slopes: Optional[Tensor],
+        softcap: float, bias: float, post_scale: float) -> Tuple[Tensor, Tensor]:
+    from .attention import _prepare
+
+    p = _params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap, bias,
+                post_scale)
+    o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)  # contiguous, as the fake
+    a, _, _, _, _ = _prepare(q, k, v, o, **p)
+    B, H, S, _ = q.shape
+    if norm == "softmax":
+        lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device)
+    else:
+        lse = torch.empty(0, dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        _lib.fwd_lse(a, lse.data_ptr() if lse.numel() else 0, torch.cuda.current_stream(q.device).cuda_stream)
+    return o, lse
+
+
+@fwd.register_fake
+def _fwd_fake(q, k, v, norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap,
+              bias, post_scale):
+    torch._check(q.dim() == 4, lambda: "q must be 4-D [B, H, S, D]")
+    B, H, S, _ = q.shape
+    lse_shape = (B, H, S) if norm == "softmax" else (0,)
+    return torch.empty_like(q, memory_format=torch.contiguous_format), q.new_empty(lse_shape, dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{NAMESPACE}::bwd", mutates_args=(), device_types="cuda")
+def bwd(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, norm: str, causal: bool, window: int,
+        dilation: int, block: int, prefix: int, scale: Optional[float], head_scale: Optional[Tensor],
+        alibi_slopes: Optional[Tensor], softcap: float, bias: float, post_scale: float
+        ) -> Tuple[Tensor, Tensor, Tensor]:
+    from .attention import run_backward
+
+    p = _params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap, bias,
+                post_scale)
+    return run_backward(do, q, k, v, o, lse if lse.numel() else None, p)
+
+
+@bwd.register_fake
+def _bwd_fake(do, q, k, v, o, lse, norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes,
+              softcap, bias, post_scale):
+    return (torch.empty_like(q, memory_format=torch.contiguous_format),
+            torch.empty_like(k, memory_format=torch.contiguous_format),
+            torch.empty_like(v, memory_format=torch.contiguous_format))
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, *rest = inputs
+    o, lse = output
+    ctx.rest = rest  # norm .. post_scale, schema order (per-head tensors included)
+    ctx.save_for_backward(q, k, v, o, lse)
+    ctx.mark_non_differentiable(lse)
+    ctx.set_materialize_grads(False)  # no zero-filled gradient for the unused lse
+
+
+def _backward(ctx, do, _dlse):
+    q, k, v, o, lse = ctx.saved_tensors
+    if do is None:
+        return (None,) * (3 + len(ctx.rest))
+    dq, dk, dv = torch.ops.chia_attn.bwd(do, q, k, v, o, lse, *ctx.rest)
+    return (dq, dk, dv) + (None,) * len(ctx.rest)
+
+
+fwd.register_autograd(_backward, setup_context=_setup_context)
+
+
+def call_fwd(q: Tensor, k: Tensor, v: Tensor, params: dict) -> Tuple[Tensor, Tensor]:
+    """torch.ops.chia_attn.fwd with attention()'s keyword parameters (per-head
+    vectors already float32 device tensors or None; scale None = default)."""
+    return torch.ops.chia_attn.fwd(q, k, v, params["norm"], bool(params["causal"]), int(params["window"] or 0),
+                                   int(params["dilation"] or 1), int(params["block"] or 0),
+                                   int(params["prefix"] or 0),
+                                   None if params["scale"] is None else float(params["scale"]),
+                                   params["head_scale"], params["alibi_slopes"], float(params["softcap"] or 0.0),
+                                   float(params["bias"]), float(params["post_scale"]))
