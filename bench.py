@@ -158,6 +158,86 @@ def backward_report(cases, inputs, works, args) -> int:
     return 0
 
 
+def flex_description(op: str, H: int, params: dict):
+    """(score_mod, mask_mod, norm kwargs) for variant `op` with the suite's parameters,
+    written as FlexAttention callables (extra_bench.py:85-95 style; sigmoid / ReLU via norm=)."""
+    import torch
+
+    p = dict(params)
+    causal = lambda b, h, q, k: k <= q  # noqa: E731
+    if op == "bias_sliding_window":
+        w = p["window"]
+        return None, lambda b, h, q, k: (k <= q) & (q - k < w), {}
+    if op == "bias_local":
+        w = p["window"]
+        return None, lambda b, h, q, k: (q - k).abs() < w, {}
+    if op == "bias_dilated":
+        d, w = p["dilation"], p.get("window", 0)
+        return None, lambda b, h, q, k: (k <= q) & ((q - k) % d == 0) & ((q - k < w) if w else (q >= 0)), {}
+    if op == "bias_block_diagonal":
+        blk, c = p["block"], p.get("causal", True)
+        return None, lambda b, h, q, k: (q // blk == k // blk) & ((k <= q) if c else (q >= 0)), {}
+    if op == "bias_prefix_lm":
+        pre = p["prefix"]
+        return None, lambda b, h, q, k: (k <= q) | (k < pre), {}
+    if op == "bias_alibi":
+        sl = torch.as_tensor(p["slopes"], dtype=torch.float32)
+        return (lambda s, b, h, q, k: s + sl[h] * (k - q)), causal, {}
+    if op == "softcap_gemma2":
+        cap = p["softcap"]
+        return (lambda s, b, h, q, k: torch.tanh(s / cap) * cap), causal, {}
+    if op == "temp_perhead":
+        t = torch.as_tensor(p["temperature"], dtype=torch.float32)
+        if p.get("mode", "mul") == "div":
+            return (lambda s, b, h, q, k: s / t[h]), causal, {}
+        return (lambda s, b, h, q, k: s * t[h]), causal, {}
+    if op == "relu_attn":
+        return None, (None if not p.get("causal", True) else causal), dict(norm="relu", post_scale=p["post_scale"])
+    if op == "sigmoid_attn":
+        return None, (None if not p.get("causal", True) else causal), dict(norm="sigmoid", bias=p["bias"])
+    raise KeyError(op)
+
+
+def flex_report(cases, inputs, calls, args) -> int:
+    """Per variant: the FlexAttention-style front end (chia_proj_amd.flex) against
+    the direct variant call -- compile time of the callables (mask evaluation and
+    fit, once) and HIP-event median per call of each path; the compiled call must
+    return the direct call's output bit for bit."""
+    import time
+
+    import torch
+
+    from chia_proj_amd.flex import create_block_mask, fit_score_mod, flex_attention
+    from chia_proj_amd.timing import median_us
+
+    rows = {}
+    for c in cases:
+        q, k, v, params = inputs[c.name]
+        score_mod, mask_mod, norm_kw = flex_description(c.op, c.H, params)
+        t0 = time.perf_counter()
+        bm = create_block_mask(mask_mod, c.B, c.H, c.S, c.S, device=q.device) if mask_mod is not None else None
+        fitted = fit_score_mod(score_mod, c.H, c.S, batch=c.B) if score_mod is not None else None
+        compile_ms = (time.perf_counter() - t0) * 1e3
+        flex_call = lambda: flex_attention(q, k, v, score_mod=fitted, block_mask=bm, **norm_kw)  # noqa: E731
+        same = bool(torch.equal(flex_call(), calls[c.name]()))
+        us_flex = median_us(flex_call)
+        us_direct = median_us(calls[c.name])
+        rows[c.op] = {"flex_us": round(us_flex, 2), "direct_us": round(us_direct, 2),
+                      "compile_ms": round(compile_ms, 1), "identical_output": same,
+                      "mask": bm.mask_kwargs() if bm is not None else None}
+        log(f"  flex {c.op:22s} flex {us_flex:8.1f} us  direct {us_direct:8.1f} us  compile {compile_ms:7.1f} ms  "
+            f"identical={same}")
+    c0 = cases[0]
+    print(json.dumps({
+        "metric": "flex_attention front end us/call vs the direct variant call", "unit": "us",
+        "higher_is_better": False, "dtype": "bf16", "data": "synthetic", "n_gpus": 1,
+        "config": {"workload": f"ten variants as FlexAttention callables, B{c0.B} H{c0.H} S{c0.S} D{c0.D} bf16",
+                   "suite": args.suite},
+        "variants": rows,
+    }), flush=True)
+    return 0 if all(r["identical_output"] for r in rows.values()) else 1
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +252,9 @@ def main() -> int:
     ap.add_argument("--backward", action="store_true",
                     help="time the backward (chia_attn_bwd: dq, dk, dv) of each variant instead of the forward step; "
                          "prints its own JSON line (not the headline metric)")
+    ap.add_argument("--flex", action="store_true",
+                    help="time the FlexAttention-style front end (score_mod / mask_mod callables compiled to the "
+                         "core) against the direct variant calls; prints its own JSON line")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
                          "kernel that reads and writes 512 MiB, and exit (with --backward: two backward passes per variant)")
@@ -210,6 +293,8 @@ def main() -> int:
         works[c.name] = work(c.op, c.B, c.H, c.S, c.D, params)
     if args.backward:
         return backward_report(cases, inputs, works, args)
+    if args.flex:
+        return flex_report(cases, inputs, calls, args)
     outputs = {c.name: calls[c.name]() for c in cases}
     torch.cuda.synchronize()
 

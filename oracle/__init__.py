@@ -14,6 +14,9 @@ Modules
                score modifier / normaliser), used for edge cases the ten
                fixed variants do not reach.
   brute.py     float64 NumPy loops over (i, j) for tiny shapes.
+  grad.py      the backward: autograd of generic.py's forward (dq, dk, dv).
+  flex.py      FlexAttention's score_mod / mask_mod callables applied literally
+               on the dense grid (the checker of chia_proj_amd.flex).
 
 How each part is pinned (tests/test_oracle_*.py):
   * reductions to torch.nn.functional.scaled_dot_product_attention (an
@@ -26,6 +29,10 @@ How each part is pinned (tests/test_oracle_*.py):
   * the masks against the reference's own lambdas restated verbatim;
   * unmasked-fraction figures quoted from the reference's configuration
     analysis (11.72 % window-256 at S=2048, 53.13 % prefix-1024 at S=4096 ...).
+  * grad.py: finite differences (gradcheck, float64) and SDPA's backward;
+  * flex.py: equals generic.py on the reference's FlexAttention descriptions
+    and on random mask parameter sets (the callables built from the
+    definitions), and SDPA for plain causal softmax.
 The reference holds no tensor-valued golden vectors (its results/ hold only
 latencies and relative errors), so these checks are the pins.
 """
