@@ -238,6 +238,54 @@ def flex_report(cases, inputs, calls, args) -> int:
     return 0 if all(r["identical_output"] for r in rows.values()) else 1
 
 
+def varlen_report(args) -> int:
+    """Packed variable-length batch (attention_varlen): causal softmax, H16 D64,
+    sequence lengths drawn in [256, 4096] up to 16384 tokens (the north-star
+    shape's token count).  HIP-event median per call and algorithmic TFLOP/s
+    (4 D per visible pair, summed over sequences), beside the same sequences
+    padded to the longest (one fixed-length launch) and launched one by one."""
+    import torch
+
+    from chia_proj_amd import attention, attention_varlen, plan
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS
+    from chia_proj_amd.timing import median_us
+
+    H, D, budget = 16, 64, 16384
+    g = torch.Generator("cpu").manual_seed(2026)
+    lens = []
+    while sum(lens) < budget:
+        lens.append(min(int(torch.randint(256, 4097, (1,), generator=g)), budget - sum(lens)))
+    T, B, S = sum(lens), len(lens), max(lens)
+    q, k, v = (torch.randn(T, H, D, generator=g).to(torch.bfloat16).cuda() for _ in range(3))
+    cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    pairs = sum(plan(batch=1, heads=1, seqlen=L, head_dim=D, causal=True)["pairs_visible"] for L in lens)
+    flops = 4.0 * D * pairs * H
+    packed = lambda: attention_varlen(q, k, v, cu, S, causal=True)  # noqa: E731
+    pads = [torch.randn(B, S, H, D, generator=g).to(torch.bfloat16).cuda().transpose(1, 2) for _ in range(3)]
+    for b, (a0, a1) in enumerate(zip(cu[:-1].tolist(), cu[1:].tolist())):
+        for t, src in zip(pads, (q, k, v)):
+            t[b, :, :a1 - a0] = src[a0:a1].transpose(0, 1)
+    padded = lambda: attention(*pads, causal=True)  # noqa: E731
+    seqs = [(q[a:b].transpose(0, 1)[None], k[a:b].transpose(0, 1)[None], v[a:b].transpose(0, 1)[None])
+            for a, b in zip(cu[:-1].tolist(), cu[1:].tolist())]
+    each = lambda: [attention(*t, causal=True) for t in seqs]  # noqa: E731
+    rows = {}
+    for name, fn in (("packed", packed), ("padded_to_longest", padded), ("one_launch_per_sequence", each)):
+        us = median_us(fn)
+        tf = flops / (us * 1e-6) / 1e12
+        rows[name] = {"us": round(us, 2), "tflops_alg": round(tf, 2),
+                      "pct_mfma_peak_alg": round(100 * tf / PEAK_BF16_TFLOPS, 2)}
+        log(f"  varlen {name:26s} {us:9.1f} us  alg {tf:7.1f} TF/s")
+    print(json.dumps({
+        "metric": "packed variable-length causal softmax, algorithmic TFLOP/s", "value": rows["packed"]["tflops_alg"],
+        "unit": "TFLOP/s", "higher_is_better": True, "dtype": "bf16", "data": "synthetic", "n_gpus": 1,
+        "config": {"workload": f"{B} sequences of 256..4096 tokens ({T} tokens), H{H} D{D}, causal softmax",
+                   "lengths": lens},
+        "paths": rows,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +303,9 @@ def main() -> int:
     ap.add_argument("--flex", action="store_true",
                     help="time the FlexAttention-style front end (score_mod / mask_mod callables compiled to the "
                          "core) against the direct variant calls; prints its own JSON line")
+    ap.add_argument("--varlen", action="store_true",
+                    help="time a packed variable-length batch (attention_varlen) against padding and per-sequence "
+                         "launches; prints its own JSON line")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
                          "kernel that reads and writes 512 MiB, and exit (with --backward: two backward passes per variant)")
@@ -277,6 +328,8 @@ def main() -> int:
         return 1
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if args.varlen:
+        return varlen_report(args)
     cases = headline_suite() if args.suite == "headline" else north_star_suite()
     if args.variants:
         keep = set(args.variants.split(","))

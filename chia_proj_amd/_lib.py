@@ -17,7 +17,7 @@ NORM_SIGMOID = 1
 NORM_RELU = 2
 NORMS = {"softmax": NORM_SOFTMAX, "sigmoid": NORM_SIGMOID, "relu": NORM_RELU}
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Entry points declared in include/chia_attn.h (checked by the CPU tests).
 EXPORTS = (
@@ -65,7 +65,10 @@ class AttnArgs(ctypes.Structure):
         ("head_scale", ctypes.c_void_p),
         ("alibi_slopes", ctypes.c_void_p),
         ("kv_heads", ctypes.c_int32),
-        ("reserved", ctypes.c_int32 * 7),
+        ("reserved0", ctypes.c_int32),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("seq_order", ctypes.c_void_p),
+        ("reserved", ctypes.c_int32 * 2),
     ]
 
     def __init__(self, **kw):

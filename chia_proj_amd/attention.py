@@ -13,6 +13,7 @@ from __future__ import annotations
 import ctypes
 import math
 import threading
+import weakref
 from collections import OrderedDict
 from typing import Optional, Sequence, Union
 
@@ -193,6 +194,24 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
     return o
 
 
+def _check_params(D, norm, window, dilation, block, prefix, scale, softcap) -> float:
+    """Host checks of the head dim and scalar parameters; returns the resolved scale."""
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS}, got {D}")
+    if norm not in _lib.NORMS:
+        raise ValueError(f"norm must be one of {sorted(_lib.NORMS)}, got {norm!r}")
+    if window < 0 or block < 0 or prefix < 0 or dilation < 1:
+        raise ValueError("window, block, prefix must be >= 0 and dilation >= 1")
+    if dilation > 1 and prefix > 0:
+        raise ValueError("prefix cannot be combined with dilation > 1")
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    if not (sc > 0 and math.isfinite(sc)):
+        raise ValueError(f"scale must be finite and > 0, got {scale}")
+    if softcap < 0 or not math.isfinite(softcap):
+        raise ValueError(f"softcap must be finite and >= 0, got {softcap}")
+    return sc
+
+
 def _prepare(q, k, v, out, *, norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes,
              softcap, bias, post_scale):
     """Validate, make the layouts the kernel takes, allocate o and fill the argument struct."""
@@ -210,21 +229,9 @@ def _prepare(q, k, v, out, *, norm, causal, window, dilation, block, prefix, sca
     if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
         raise ValueError(f"q, k, v must be on the same GPU device, got {q.device}, {k.device}, {v.device}")
     B, H, S, D = q.shape
-    if D not in SUPPORTED_HEAD_DIMS:
-        raise ValueError(f"head_dim must be one of {SUPPORTED_HEAD_DIMS}, got {D}")
     if min(B, H, S) < 1:
         raise ValueError(f"empty tensor shape {tuple(q.shape)}")
-    if norm not in _lib.NORMS:
-        raise ValueError(f"norm must be one of {sorted(_lib.NORMS)}, got {norm!r}")
-    if window < 0 or block < 0 or prefix < 0 or dilation < 1:
-        raise ValueError("window, block, prefix must be >= 0 and dilation >= 1")
-    if dilation > 1 and prefix > 0:
-        raise ValueError("prefix cannot be combined with dilation > 1")
-    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
-    if not (sc > 0 and math.isfinite(sc)):
-        raise ValueError(f"scale must be finite and > 0, got {scale}")
-    if softcap < 0 or not math.isfinite(softcap):
-        raise ValueError(f"softcap must be finite and >= 0, got {softcap}")
+    sc = _check_params(D, norm, window, dilation, block, prefix, scale, softcap)
 
     q_, k_, v_ = (t if _layout_ok(t) else t.contiguous() for t in (q, k, v))
     if out is None:
@@ -292,6 +299,197 @@ def run_backward(do, q, k, v, o, lse, params):
         st[0], st[1], st[2] = _strides3(t)
     with torch.cuda.device(q_.device):
         _lib.bwd(b, torch.cuda.current_stream(q_.device).cuda_stream)
+    return dq, dk, dv
+
+
+# ---- packed variable-length batches -------------------------------------------
+
+def _layout_ok_packed(t: torch.Tensor) -> bool:
+    return t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0
+
+
+def check_cu_seqlens(cu_seqlens, total: int, max_seqlen: Optional[int] = None) -> tuple:
+    """Host check of packed-sequence offsets: a 1-D integer tensor [B + 1] with
+    cu[0] = 0, non-decreasing, cu[B] = total tokens.  Returns (B, max length)
+    (max_seqlen if given, which must be >= every length).  Reads the values on the
+    host (a device tensor is copied back: one synchronisation)."""
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor of batch + 1 token offsets")
+    if cu_seqlens.dtype.is_floating_point or cu_seqlens.dtype == torch.bool:
+        raise TypeError(f"cu_seqlens must be an integer tensor, got {cu_seqlens.dtype}")
+    host = cu_seqlens.detach().to("cpu", torch.int64)
+    lens = host[1:] - host[:-1]
+    if int(host[0]) != 0 or bool((lens < 0).any()) or int(host[-1]) != total:
+        raise ValueError(f"cu_seqlens must start at 0, be non-decreasing and end at the {total} packed tokens")
+    if total >= (1 << 31):
+        raise ValueError("at most 2^31 - 1 packed tokens")
+    longest = int(lens.max())
+    if max_seqlen is not None:
+        if int(max_seqlen) < longest:
+            raise ValueError(f"max_seqlen {max_seqlen} is shorter than the longest sequence ({longest})")
+        longest = int(max_seqlen)
+    return int(lens.numel()), longest
+
+
+_CU_CACHE_MAX = 32
+_cu_cache: "OrderedDict[tuple, tuple]" = OrderedDict()
+
+
+def _cu_plan(cu_seqlens, total: int, max_seqlen: Optional[int], device):
+    """(B, max length, int32 device offsets, device dispatch order) for a checked
+    cu_seqlens.  The check reads the offsets on the host (a device tensor: one
+    synchronisation); the result is cached per tensor storage and version, so a
+    cu_seqlens reused unchanged (every layer of a model) is checked once.  The
+    order puts the longest sequences first (a shorter tail of the launch)."""
+    key = None
+    if isinstance(cu_seqlens, torch.Tensor) and not torch.compiler.is_compiling():
+        # the same live tensor object (a weak reference guards against a new
+        # tensor at a recycled id) at the same version
+        key = (id(cu_seqlens), cu_seqlens._version, total, max_seqlen, str(device))
+        hit = _cu_cache.get(key)
+        if hit is not None and hit[0]() is cu_seqlens:
+            _cu_cache.move_to_end(key)
+            return hit[1]
+    B, S = check_cu_seqlens(cu_seqlens, total, max_seqlen)
+    host = cu_seqlens.detach().to("cpu", torch.int64)
+    order = torch.argsort(host[1:] - host[:-1], descending=True, stable=True).to(torch.int32).to(device)
+    cu = host.to(torch.int32).to(device)
+    out = (B, S, cu, order)
+    if key is not None:
+        _cu_cache[key] = (weakref.ref(cu_seqlens), out)
+        if len(_cu_cache) > _CU_CACHE_MAX:
+            _cu_cache.popitem(last=False)
+    return out
+
+
+def _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, out, *, norm, causal, window, dilation, block, prefix, scale,
+                    head_scale, alibi_slopes, softcap, bias, post_scale):
+    """_prepare for packed q [T, H, D], k / v [T, H_kv, D]; also returns the int32
+    device copy of cu_seqlens the argument struct points at (keep it alive)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dim() != 3:
+            raise ValueError(f"{name} must be a packed 3-D [T, heads, D] tensor")
+    T, H, D = q.shape
+    if (k.shape != v.shape or k.shape[0] != T or k.shape[2] != D or k.shape[1] < 1 or H % k.shape[1] != 0):
+        raise ValueError(f"k and v must be [T, H_kv, D] with H_kv dividing q's H, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError(f"q, k, v must be bfloat16, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
+        raise ValueError(f"q, k, v must be on the same GPU device, got {q.device}, {k.device}, {v.device}")
+    B, S, cu, order = _cu_plan(cu_seqlens, T, max_seqlen, q.device)
+    sc = _check_params(D, norm, window, dilation, block, prefix, scale, softcap)
+    q_, k_, v_ = (t if _layout_ok_packed(t) else t.contiguous() for t in (q, k, v))
+    if out is None:
+        o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    else:
+        if out.shape != q.shape or out.dtype != torch.bfloat16 or out.device != q.device or not _layout_ok_packed(out):
+            raise ValueError("out must be a bf16 [T, H, D] tensor like q with unit last stride and 16-byte alignment")
+        o = out
+    hs = _per_head_vector(head_scale, H, q.device, "head_scale", positive=True)
+    sl = _per_head_vector(alibi_slopes, H, q.device, "alibi_slopes", positive=False)
+    a = make_args(batch=B, heads=H, seqlen=max(S, 1), head_dim=D, norm=norm, causal=causal, window=window,
+                  dilation=dilation, block=block, prefix=prefix, scale=sc, softcap=softcap, bias=bias,
+                  post_scale=post_scale)
+    a.q, a.k, a.v, a.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
+    a.kv_heads = k_.shape[1] if k_.shape[1] != H else 0
+    for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = 0, t.stride(1), t.stride(0)
+    a.head_scale = hs.data_ptr() if hs is not None else None
+    a.alibi_slopes = sl.data_ptr() if sl is not None else None
+    a.cu_seqlens = cu.data_ptr()
+    a.seq_order = order.data_ptr()
+    return a, (hs, sl, cu, order), (q_, k_, v_), o
+
+
+def attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                     max_seqlen: Optional[int] = None, *, norm: str = "softmax", causal: bool = True,
+                     window: int = 0, dilation: int = 1, block: int = 0, prefix: int = 0,
+                     scale: Optional[float] = None, head_scale: PerHead = None, alibi_slopes: PerHead = None,
+                     softcap: float = 0.0, bias: float = 0.0, post_scale: float = 1.0,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """attention() over a packed batch of variable-length sequences.
+
+    q [T, H, D], k / v [T, H_kv, D] bf16 on the GPU; cu_seqlens [B + 1] integer
+    token offsets (sequence b is tokens cu_seqlens[b] .. cu_seqlens[b+1]-1; empty
+    sequences allowed).  Every sequence is attended on its own, with the mask and
+    ALiBi positions counted from its first token; the parameters are attention()'s.
+    Returns o [T, H, D].  cu_seqlens is checked on the host (a device tensor is
+    copied back: one synchronisation), once per tensor and version -- reusing
+    the same unchanged tensor skips it; max_seqlen defaults to the longest sequence.
+    """
+    params = dict(norm=norm, causal=causal, window=window, dilation=dilation, block=block, prefix=prefix,
+                  scale=scale, head_scale=head_scale, alibi_slopes=alibi_slopes, softcap=softcap, bias=bias,
+                  post_scale=post_scale)
+    needs_grad = torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v))
+    if needs_grad or torch.compiler.is_compiling():
+        if out is not None:
+            raise ValueError("out= is not supported when q, k or v requires grad or under torch.compile")
+        return _op_forward_varlen(q, k, v, cu_seqlens, max_seqlen, params)[0]
+    if isinstance(q, torch.Tensor) and q.dim() == 3 and q.shape[0] == 0:
+        check_cu_seqlens(cu_seqlens, 0, max_seqlen)
+        return torch.empty_like(q) if out is None else out
+    a, keep, _, o = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, out, **params)
+    with torch.cuda.device(q.device):
+        _lib.fwd(a, torch.cuda.current_stream(q.device).cuda_stream)
+    del keep  # the launch is queued; torch's allocator orders any reuse after it on this stream
+    return o
+
+
+def _op_forward_varlen(q, k, v, cu_seqlens, max_seqlen, params):
+    """(o, lse [T, H]) through torch.ops.chia_attn.fwd_varlen."""
+    from .library import call_fwd_varlen
+
+    if not isinstance(q, torch.Tensor) or q.dim() != 3:
+        raise ValueError("q must be a packed 3-D [T, heads, D] tensor")
+    p = dict(params)
+    H = q.shape[1]
+    cache = (q.device.type == "cuda" and not torch.compiler.is_compiling()
+             and not isinstance(q, torch._subclasses.fake_tensor.FakeTensor))
+    p["head_scale"] = _per_head_vector(p["head_scale"], H, q.device, "head_scale", positive=True, cache=cache)
+    p["alibi_slopes"] = _per_head_vector(p["alibi_slopes"], H, q.device, "alibi_slopes", positive=False,
+                                         cache=cache)
+    return call_fwd_varlen(q, k, v, cu_seqlens, max_seqlen, p)
+
+
+def run_forward_varlen(q, k, v, cu_seqlens, max_seqlen, params):
+    """(o, lse) for the registered operator: lse float32 [T, H] (softmax) or [0]."""
+    T, H, _ = q.shape
+    o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    softmax = params["norm"] == "softmax"
+    lse = torch.empty(T if softmax else 0, H if softmax else 0, dtype=torch.float32, device=q.device)
+    if T == 0:
+        check_cu_seqlens(cu_seqlens, 0, max_seqlen)
+        return o, lse
+    a, keep, _, _ = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, o, **params)
+    with torch.cuda.device(q.device):
+        _lib.fwd_lse(a, lse.data_ptr() if softmax else 0, torch.cuda.current_stream(q.device).cuda_stream)
+    del keep
+    return o, lse
+
+
+def run_backward_varlen(do, q, k, v, o, lse, cu_seqlens, max_seqlen, params):
+    """dq, dk, dv of a packed batch by chia_attn_bwd."""
+    dq, dk, dv = (torch.empty(t.shape, dtype=torch.bfloat16, device=t.device) for t in (q, k, v))
+    if q.shape[0] == 0:
+        return dq, dk, dv
+    a, keep, _, _ = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, o, **params)
+    do_ = do if (do.dtype == torch.bfloat16 and _layout_ok_packed(do)) else do.to(torch.bfloat16).contiguous()
+    if do_.shape != q.shape:
+        raise ValueError(f"do must have q's shape {tuple(q.shape)}, got {tuple(do.shape)}")
+    softmax = params["norm"] == "softmax"
+    nbytes = _lib.bwd_workspace_size(a)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    b = _lib.BwdArgs(dout=do_.data_ptr(), dq=dq.data_ptr(), dk=dk.data_ptr(), dv=dv.data_ptr(),
+                     lse=lse.data_ptr() if softmax else None, workspace=ws.data_ptr(), workspace_bytes=nbytes)
+    b.fwd = ctypes.pointer(a)
+    for name, t in (("dout_stride", do_), ("dq_stride", dq), ("dk_stride", dk), ("dv_stride", dv)):
+        st = getattr(b, name)
+        st[0], st[1], st[2] = 0, t.stride(1), t.stride(0)
+    with torch.cuda.device(q.device):
+        _lib.bwd(b, torch.cuda.current_stream(q.device).cuda_stream)
+    del keep
     return dq, dk, dv
 
 

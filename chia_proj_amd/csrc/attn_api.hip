@@ -44,14 +44,17 @@ int validate(const chia_attn_args* a, bool need_tensors) {
   if (!(a->scale > 0.f) || !std::isfinite(a->scale)) return CHIA_ATTN_ERR_SCALE;
   if (!(a->softcap >= 0.f) || !std::isfinite(a->softcap)) return CHIA_ATTN_ERR_SCALE;
   if (!std::isfinite(a->bias) || !std::isfinite(a->post_scale)) return CHIA_ATTN_ERR_SCALE;
-  for (int i = 0; i < 7; ++i)
+  if (a->reserved0 != 0) return CHIA_ATTN_ERR_STRUCT;
+  for (int i = 0; i < 2; ++i)
     if (a->reserved[i] != 0) return CHIA_ATTN_ERR_STRUCT;
   if (a->kv_heads < 0 || (a->kv_heads > 0 && a->heads % a->kv_heads != 0)) return CHIA_ATTN_ERR_SHAPE;
   if (need_tensors) {
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o)) return CHIA_ATTN_ERR_ALIGN;
     if (!stride_ok(a->q_stride) || !stride_ok(a->k_stride) || !stride_ok(a->v_stride) || !stride_ok(a->o_stride))
       return CHIA_ATTN_ERR_ALIGN;
-    if (((uintptr_t)a->head_scale & 3u) || ((uintptr_t)a->alibi_slopes & 3u)) return CHIA_ATTN_ERR_ALIGN;
+    if (((uintptr_t)a->head_scale & 3u) || ((uintptr_t)a->alibi_slopes & 3u) || ((uintptr_t)a->cu_seqlens & 3u) ||
+        ((uintptr_t)a->seq_order & 3u))
+      return CHIA_ATTN_ERR_ALIGN;
     // K/V tile loads address a tile's rows with 32-bit byte offsets from the
     // tile's first row: 64 rows x (seq stride x dilation) x 2 bytes < 2^32.
     for (const int64_t* st : {a->k_stride, a->v_stride})
@@ -59,6 +62,10 @@ int validate(const chia_attn_args* a, bool need_tensors) {
   }
   return CHIA_ATTN_OK;
 }
+
+// Packed sequences step through tokens with stride[2] from each sequence's
+// first token; the batch stride is not used.
+int64_t batch_stride(const chia_attn_args* a, const int64_t* st) { return a->cu_seqlens ? 0 : st[0]; }
 
 MaskSpec spec_of(const chia_attn_args* a) {
   return make_mask_spec((int32_t)a->seqlen, a->causal ? 1 : 0, a->window, a->dilation, a->block, a->prefix);
@@ -142,15 +149,21 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   p.k = (const uint16_t*)a->k;
   p.v = (const uint16_t*)a->v;
   p.o = (uint16_t*)a->o;
-  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
-  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
-  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
-  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.q_sb = batch_stride(a, a->q_stride); p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
+  p.k_sb = batch_stride(a, a->k_stride); p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
+  p.v_sb = batch_stride(a, a->v_stride); p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
+  p.o_sb = batch_stride(a, a->o_stride); p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
   p.head_scale = a->head_scale;
   p.alibi_slopes = a->alibi_slopes;
   p.mask = spec_of(a);
   p.B = (int32_t)a->batch;
   p.H = (int32_t)a->heads;
+  p.cu_seqlens = a->cu_seqlens;
+  p.seq_order = a->cu_seqlens ? a->seq_order : nullptr;
+  // lse: [B, H, S], or [T, H] for packed sequences
+  p.lse_sb = a->cu_seqlens ? 0 : a->heads * a->seqlen;
+  p.lse_sh = a->cu_seqlens ? 1 : a->seqlen;
+  p.lse_ss = a->cu_seqlens ? a->heads : 1;
   const Geometry geo = geometry_of(p.mask, a->batch, a->heads);
   p.residues = geo.residues;
   p.n_pairs = geo.n_pairs;
@@ -258,15 +271,20 @@ extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
   p.dq = (uint16_t*)ba->dq;
   p.dk = (uint16_t*)ba->dk;
   p.dv = (uint16_t*)ba->dv;
-  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
-  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
-  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
-  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
-  p.do_sb = ba->dout_stride[0]; p.do_sh = ba->dout_stride[1]; p.do_ss = ba->dout_stride[2];
-  p.dq_sb = ba->dq_stride[0]; p.dq_sh = ba->dq_stride[1]; p.dq_ss = ba->dq_stride[2];
-  p.dk_sb = ba->dk_stride[0]; p.dk_sh = ba->dk_stride[1]; p.dk_ss = ba->dk_stride[2];
-  p.dv_sb = ba->dv_stride[0]; p.dv_sh = ba->dv_stride[1]; p.dv_ss = ba->dv_stride[2];
+  p.q_sb = batch_stride(a, a->q_stride); p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
+  p.k_sb = batch_stride(a, a->k_stride); p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
+  p.v_sb = batch_stride(a, a->v_stride); p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
+  p.o_sb = batch_stride(a, a->o_stride); p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.do_sb = batch_stride(a, ba->dout_stride); p.do_sh = ba->dout_stride[1]; p.do_ss = ba->dout_stride[2];
+  p.dq_sb = batch_stride(a, ba->dq_stride); p.dq_sh = ba->dq_stride[1]; p.dq_ss = ba->dq_stride[2];
+  p.dk_sb = batch_stride(a, ba->dk_stride); p.dk_sh = ba->dk_stride[1]; p.dk_ss = ba->dk_stride[2];
+  p.dv_sb = batch_stride(a, ba->dv_stride); p.dv_sh = ba->dv_stride[1]; p.dv_ss = ba->dv_stride[2];
+  p.cu_seqlens = a->cu_seqlens;
+  p.seq_order = a->cu_seqlens ? a->seq_order : nullptr;
   p.lse = softmax ? ba->lse : nullptr;
+  p.lse_sb = a->cu_seqlens ? 0 : a->heads * a->seqlen;
+  p.lse_sh = a->cu_seqlens ? 1 : a->seqlen;
+  p.lse_ss = a->cu_seqlens ? a->heads : 1;
   p.stats = softmax ? (float*)ba->workspace : nullptr;
   p.head_scale = a->head_scale;
   p.alibi_slopes = a->alibi_slopes;

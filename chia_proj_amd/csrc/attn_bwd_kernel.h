@@ -62,7 +62,10 @@ struct BwdParams {
   int64_t dq_sb, dq_sh, dq_ss;
   int64_t dk_sb, dk_sh, dk_ss;
   int64_t dv_sb, dv_sh, dv_ss;
-  const float* lse;     // softmax: [B, H, S], natural log
+  const float* lse;     // softmax: natural log, strides lse_sb / lse_sh / lse_ss
+  int64_t lse_sb, lse_sh, lse_ss;
+  const int32_t* cu_seqlens;  // packed sequences: [B + 1] token offsets, or nullptr
+  const int32_t* seq_order;   // packed sequences: dispatch order of the B sequences, or nullptr
   float* stats;         // softmax: [B, H, R, SR] lse log2 e, then [B, H, R, SR] delta
   const float* head_scale;
   const float* alibi_slopes;
@@ -190,8 +193,11 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdParams p) 
   const int bh = (int)(idx / S);
   const int i = (int)(idx - (int64_t)bh * S);
   const int b = udiv(bh, p.div_h), h = bh - b * p.H;
-  const uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + (int64_t)i * p.o_ss;
-  const uint16_t* drow = p.dout + b * p.do_sb + h * p.do_sh + (int64_t)i * p.do_ss;
+  const SeqSpan seq = seq_span(p.cu_seqlens, b, S);
+  if (i >= seq.len) return;
+  const int64_t t = seq.tok0 + i;
+  const uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + t * p.o_ss;
+  const uint16_t* drow = p.dout + b * p.do_sb + h * p.do_sh + t * p.do_ss;
   float acc = 0.f;
 #pragma unroll
   for (int c = 0; c < D / 8; ++c) {
@@ -206,7 +212,7 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdParams p) 
   const int ir = udiv(i, p.div_dil), r = i - ir * p.mask.dil;
   const int64_t o2 = ((int64_t)bh * p.residues + r) * p.SR + ir;
   const int64_t plane = (int64_t)p.B * p.H * p.residues * p.SR;
-  p.stats[o2] = p.lse[idx] * kLog2e;
+  p.stats[o2] = p.lse[b * p.lse_sb + h * p.lse_sh + t * p.lse_ss] * kLog2e;
   p.stats[plane + o2] = acc;
 }
 
@@ -223,21 +229,27 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   const int lq = lane & 31, lh = lane >> 5;
 
   // workgroup -> (b, h, residue, 128-row block), heaviest blocks first
-  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  // (packed sequences of unequal length: round-robin over the XCDs, no remap)
+  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
   const int bhr = udiv(L, p.div_blk);
   const int blk = p.n_blk - 1 - (L - bhr * p.n_blk);
   const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
-  const int b = udiv(bh, p.div_h), h = bh - b * p.H;
-  const MaskGeom g = residue_geom(p.mask, r);
+  const int bs = udiv(bh, p.div_h), h = bh - bs * p.H;
+  const int b = seq_of(p.seq_order, bs);
+  const SeqSpan seq = seq_span(p.cu_seqlens, b, p.mask.S);
+  MaskSpec ms = p.mask;
+  ms.S = seq.len;
+  const MaskGeom g = residue_geom(ms, r);
   const int nblk_r = (g.S + 127) / 128;
   if (blk >= nblk_r) return;  // whole workgroup, before any barrier
   const int hkv = udiv(h, p.div_g);
   const int dil = p.mask.dil;
-  const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
-  const uint16_t* doh = p.dout + b * p.do_sb + h * p.do_sh + r * p.do_ss;
-  const uint16_t* kh = p.k + b * p.k_sb + hkv * p.k_sh + r * p.k_ss;
-  const uint16_t* vh = p.v + b * p.v_sb + hkv * p.v_sh + r * p.v_ss;
-  uint16_t* dqh = p.dq + b * p.dq_sb + h * p.dq_sh + r * p.dq_ss;
+  const int64_t t0 = seq.tok0 + r;  // the residue's first token
+  const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + t0 * p.q_ss;
+  const uint16_t* doh = p.dout + b * p.do_sb + h * p.do_sh + t0 * p.do_ss;
+  const uint16_t* kh = p.k + b * p.k_sb + hkv * p.k_sh + t0 * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hkv * p.v_sh + t0 * p.v_ss;
+  uint16_t* dqh = p.dq + b * p.dq_sb + h * p.dq_sh + t0 * p.dq_ss;
   const int64_t qrs = p.q_ss * dil, dors = p.do_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil,
                 dqrs = p.dq_ss * dil;
   ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
@@ -260,7 +272,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   }
   float lse2 = 0.f, delta = 0.f;
   if constexpr (NORM == NORM_SOFTMAX) {
-    const int64_t o2 = ((int64_t)bh * p.residues + r) * p.SR + (ok ? i : 0);
+    const int64_t o2 = ((int64_t)(b * p.H + h) * p.residues + r) * p.SR + (ok ? i : 0);  // b: the sequence
     lse2 = p.stats[o2];
     delta = p.stats[(int64_t)p.B * p.H * p.residues * p.SR + o2];
   }
@@ -381,19 +393,24 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
   // workgroup -> (b, K/V head, residue, 128-key block); low blocks (seen by
   // the most rows under a causal mask) first
   const int HK = p.H / p.G;
-  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
   const int bhr = udiv(L, p.div_blk);
   const int blk = L - bhr * p.n_blk;
   const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
-  const int b = udiv(bh, p.div_hk), hkv = bh - b * HK;
-  const MaskGeom g = residue_geom(p.mask, r);
+  const int bs = udiv(bh, p.div_hk), hkv = bh - bs * HK;
+  const int b = seq_of(p.seq_order, bs);
+  const SeqSpan seq = seq_span(p.cu_seqlens, b, p.mask.S);
+  MaskSpec ms = p.mask;
+  ms.S = seq.len;
+  const MaskGeom g = residue_geom(ms, r);
   const int nblk_r = (g.S + 127) / 128;
   if (blk >= nblk_r) return;  // whole workgroup, before any barrier
   const int dil = p.mask.dil;
-  const uint16_t* kh = p.k + b * p.k_sb + hkv * p.k_sh + r * p.k_ss;
-  const uint16_t* vh = p.v + b * p.v_sb + hkv * p.v_sh + r * p.v_ss;
-  uint16_t* dkh = p.dk + b * p.dk_sb + hkv * p.dk_sh + r * p.dk_ss;
-  uint16_t* dvh = p.dv + b * p.dv_sb + hkv * p.dv_sh + r * p.dv_ss;
+  const int64_t t0 = seq.tok0 + r;  // the residue's first token
+  const uint16_t* kh = p.k + b * p.k_sb + hkv * p.k_sh + t0 * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hkv * p.v_sh + t0 * p.v_ss;
+  uint16_t* dkh = p.dk + b * p.dk_sb + hkv * p.dk_sh + t0 * p.dk_ss;
+  uint16_t* dvh = p.dv + b * p.dv_sb + hkv * p.dv_sh + t0 * p.dv_ss;
   const int64_t qrs = p.q_ss * dil, dors = p.do_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil,
                 dkrs = p.dk_ss * dil, dvrs = p.dv_ss * dil;
 
@@ -447,8 +464,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
   auto issue = [&](int it) {
     const int hq = tile_head(it), i0 = tile_row(it);
     char* st = lds + (it % NS) * STAGE_BYTES;
-    dma_rows<D, NW>(p.q + b * p.q_sb + hq * p.q_sh + r * p.q_ss, qrs, i0, g.S, st, wave, lane);
-    dma_rows<D, NW>(p.dout + b * p.do_sb + hq * p.do_sh + r * p.do_ss, dors, i0, g.S, st + T_BYTES, wave, lane);
+    dma_rows<D, NW>(p.q + b * p.q_sb + hq * p.q_sh + t0 * p.q_ss, qrs, i0, g.S, st, wave, lane);
+    dma_rows<D, NW>(p.dout + b * p.do_sb + hq * p.do_sh + t0 * p.do_ss, dors, i0, g.S, st + T_BYTES, wave, lane);
     if constexpr (kStats) {
       // wavefront w moves 32 floats: lse log2 e rows [32 w, +32) (w < 2), or
       // delta rows [32 (w - 2), +32); the stats rows are padded to 64

@@ -95,9 +95,31 @@ struct FwdParams {
   int32_t n_wg;
   UDiv div_pairs, div_res, div_h;  // dividers by n_pairs, residues, H
   UDiv div_group;                  // by query heads per K/V head (GQA / MQA)
-  float* lse;                      // softmax: fp32 [B, H, S] log-sum-exp of the scores, or nullptr
+  float* lse;                      // softmax: fp32 log-sum-exp of the scores, or nullptr
+  int64_t lse_sb, lse_sh, lse_ss;  // its strides: batch, head, token
+  const int32_t* cu_seqlens;       // packed sequences: [B + 1] token offsets, or nullptr
+  const int32_t* seq_order;        // packed sequences: dispatch order of the B sequences, or nullptr
   float scale, softcap, bias, post_scale;
 };
+
+// Packed sequences: sequence b's first token and length (at most the launch's
+// S); fixed-length batches: 0 and S.
+struct SeqSpan {
+  int64_t tok0;
+  int32_t len;
+};
+// Packed sequences: the launch's i-th sequence slot runs sequence seq_order[i].
+__device__ __forceinline__ int seq_of(const int32_t* seq_order, int i) { return seq_order ? seq_order[i] : i; }
+
+__device__ __forceinline__ SeqSpan seq_span(const int32_t* cu_seqlens, int b, int32_t S) {
+  SeqSpan s{0, S};
+  if (cu_seqlens) {
+    const int32_t t0 = cu_seqlens[b];
+    s.tok0 = t0;
+    s.len = imax32(imin32(cu_seqlens[b + 1] - t0, S), 0);
+  }
+  return s;
+}
 
 // Waves per SIMD the register budget targets: two at head_dim 64 (the
 // hardware then overlaps one wave's softmax with the other's MFMAs), one at
@@ -232,14 +254,20 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   const int lq = lane & 31, lh = lane >> 5;
 
   // ---- workgroup -> (batch, head, residue, row-block pair) -----------------
-  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  // Packed sequences of unequal length: consecutive workgroups go round-robin
+  // to the XCDs so every XCD gets a share of every sequence's work.
+  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
   const int bhr = udiv(L, p.div_pairs);
   const int pr = L - bhr * p.n_pairs;
   const int bh = udiv(bhr, p.div_res);
   const int r = bhr - bh * p.residues;
-  const int b = udiv(bh, p.div_h);
-  const int h = bh - b * p.H;
-  const MaskGeom g = residue_geom(p.mask, r);
+  const int bs = udiv(bh, p.div_h);
+  const int h = bh - bs * p.H;
+  const int b = seq_of(p.seq_order, bs);
+  const SeqSpan seq = seq_span(p.cu_seqlens, b, p.mask.S);
+  MaskSpec ms = p.mask;
+  ms.S = seq.len;
+  const MaskGeom g = residue_geom(ms, r);
   const int nblk = (g.S + BMH - 1) / BMH;  // row blocks of this residue
   int blk0, blk1;
   if (p.zigzag) {
@@ -255,11 +283,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   }
 
   const int dil = p.mask.dil;
-  const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
+  const int64_t t0 = seq.tok0 + r;  // the residue's first token
+  const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + t0 * p.q_ss;
   const int hk = udiv(h, p.div_group);  // K/V head of query head h
-  const uint16_t* kh = p.k + b * p.k_sb + hk * p.k_sh + r * p.k_ss;
-  const uint16_t* vh = p.v + b * p.v_sb + hk * p.v_sh + r * p.v_ss;
-  uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + r * p.o_ss;
+  const uint16_t* kh = p.k + b * p.k_sb + hk * p.k_sh + t0 * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hk * p.v_sh + t0 * p.v_ss;
+  uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + t0 * p.o_ss;
   const int64_t qrs = p.q_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil, ors = p.o_ss * dil;
 
   // ---- per-head score constants --------------------------------------------
@@ -934,7 +963,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       // (-inf for a row that sees no key)
       if (p.lse != nullptr && lh == 0 && valid[qb] && i < g.S) {
         const float lse2 = lt > 0.f ? m_run[qb] + __builtin_amdgcn_logf(lt) : -INFINITY;
-        p.lse[((int64_t)b * p.H + h) * p.mask.S + g.r + (int64_t)g.dil * i] = lse2 * kLn2;
+        p.lse[b * p.lse_sb + h * p.lse_sh + (t0 + (int64_t)g.dil * i) * p.lse_ss] = lse2 * kLn2;
       }
     } else {
       f = post;

@@ -115,3 +115,87 @@ def call_fwd(q: Tensor, k: Tensor, v: Tensor, params: dict) -> Tuple[Tensor, Ten
                                    None if params["scale"] is None else float(params["scale"]),
                                    params["head_scale"], params["alibi_slopes"], float(params["softcap"] or 0.0),
                                    float(params["bias"]), float(params["post_scale"]))
+
+
+# ---- packed variable-length batches ------------------------------------------------
+#   chia_attn::fwd_varlen(q, k, v, cu_seqlens, max_seqlen, <parameters>) -> (o, lse)
+#       q, o [T, H, D]; k, v [T, H_kv, D]; lse float32 [T, H] (softmax) or [0]
+#   chia_attn::bwd_varlen(do, q, k, v, o, lse, cu_seqlens, max_seqlen, <parameters>) -> (dq, dk, dv)
+# max_seqlen <= 0: the longest sequence (read from cu_seqlens on the host).
+
+def _max_len(max_seqlen: int):
+    return None if max_seqlen <= 0 else max_seqlen
+
+
+@torch.library.custom_op(f"{NAMESPACE}::fwd_varlen", mutates_args=(), device_types="cuda")
+def fwd_varlen(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: int, norm: str, causal: bool,
+               window: int, dilation: int, block: int, prefix: int, scale: Optional[float],
+               head_scale: Optional[Tensor], alibi_slopes: Optional[Tensor], softcap: float, bias: float,
+               post_scale: float) -> Tuple[Tensor, Tensor]:
+    from .attention import run_forward_varlen
+
+    p = _params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap, bias,
+                post_scale)
+    return run_forward_varlen(q, k, v, cu_seqlens, _max_len(max_seqlen), p)
+
+
+@fwd_varlen.register_fake
+def _fwd_varlen_fake(q, k, v, cu_seqlens, max_seqlen, norm, causal, window, dilation, block, prefix, scale,
+                     head_scale, alibi_slopes, softcap, bias, post_scale):
+    torch._check(q.dim() == 3, lambda: "q must be 3-D [T, H, D]")
+    T, H, _ = q.shape
+    lse_shape = (T, H) if norm == "softmax" else (0, 0)
+    return torch.empty_like(q, memory_format=torch.contiguous_format), q.new_empty(lse_shape, dtype=torch.float32)
+
+
+@torch.library.custom_op(f"{NAMESPACE}::bwd_varlen", mutates_args=(), device_types="cuda")
+def bwd_varlen(do: Tensor, q: Tensor, k: Tensor, v: Tensor, o: Tensor, lse: Tensor, cu_seqlens: Tensor,
+               max_seqlen: int, norm: str, causal: bool, window: int, dilation: int, block: int, prefix: int,
+               scale: Optional[float], head_scale: Optional[Tensor], alibi_slopes: Optional[Tensor], softcap: float,
+               bias: float, post_scale: float) -> Tuple[Tensor, Tensor, Tensor]:
+    from .attention import run_backward_varlen
+
+    p = _params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap, bias,
+                post_scale)
+    return run_backward_varlen(do, q, k, v, o, lse, cu_seqlens, _max_len(max_seqlen), p)
+
+
+@bwd_varlen.register_fake
+def _bwd_varlen_fake(do, q, k, v, o, lse, cu_seqlens, max_seqlen, norm, causal, window, dilation, block, prefix,
+                     scale, head_scale, alibi_slopes, softcap, bias, post_scale):
+    return (torch.empty_like(q, memory_format=torch.contiguous_format),
+            torch.empty_like(k, memory_format=torch.contiguous_format),
+            torch.empty_like(v, memory_format=torch.contiguous_format))
+
+
+def _setup_context_varlen(ctx, inputs, output):
+    q, k, v, cu_seqlens, *rest = inputs
+    o, lse = output
+    ctx.rest = rest  # max_seqlen .. post_scale, schema order
+    ctx.save_for_backward(q, k, v, o, lse, cu_seqlens)
+    ctx.mark_non_differentiable(lse)
+    ctx.set_materialize_grads(False)
+
+
+def _backward_varlen(ctx, do, _dlse):
+    q, k, v, o, lse, cu_seqlens = ctx.saved_tensors
+    if do is None:
+        return (None,) * (4 + len(ctx.rest))
+    dq, dk, dv = torch.ops.chia_attn.bwd_varlen(do, q, k, v, o, lse, cu_seqlens, *ctx.rest)
+    return (dq, dk, dv) + (None,) * (1 + len(ctx.rest))
+
+
+fwd_varlen.register_autograd(_backward_varlen, setup_context=_setup_context_varlen)
+
+
+def call_fwd_varlen(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seqlen: Optional[int],
+                    params: dict) -> Tuple[Tensor, Tensor]:
+    """torch.ops.chia_attn.fwd_varlen with attention_varlen()'s keyword parameters."""
+    return torch.ops.chia_attn.fwd_varlen(q, k, v, cu_seqlens, int(max_seqlen or 0), params["norm"],
+                                          bool(params["causal"]), int(params["window"] or 0),
+                                          int(params["dilation"] or 1), int(params["block"] or 0),
+                                          int(params["prefix"] or 0),
+                                          None if params["scale"] is None else float(params["scale"]),
+                                          params["head_scale"], params["alibi_slopes"],
+                                          float(params["softcap"] or 0.0), float(params["bias"]),
+                                          float(params["post_scale"]))

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define CHIA_ATTN_ABI_VERSION 2  /* 2: kv_heads (GQA / MQA) */
+#define CHIA_ATTN_ABI_VERSION 3  /* 2: kv_heads (GQA / MQA); 3: cu_seqlens (packed sequences) */
 
 /* Normaliser applied to the (modified, masked) scores.
  *   SOFTMAX: p = softmax_j(s) over visible keys   (extra_bench.py:42)
@@ -104,7 +104,25 @@ typedef struct chia_attn_args {
    * head per query head).  heads % kv_heads must be 0.  The reference's
    * kernels take K and V of q's shape only; this generalises them. */
   int32_t kv_heads;
-  int32_t reserved[7];        /* must be zero */
+  int32_t reserved0;          /* must be zero */
+
+  /* Variable-length batches (packed sequences).  NULL: every sequence has
+   * seqlen tokens and the tensors are [B, H, S, D] as above.  Otherwise a
+   * device int32[batch + 1] with cu_seqlens[0] = 0, non-decreasing: sequence b
+   * is tokens [cu_seqlens[b], cu_seqlens[b + 1]) of packed tensors q, o
+   * [T, H, D] and k, v [T, H_kv, D]; the batch strides (stride[0]) are ignored
+   * and stride[2] steps one token.  seqlen must be >= every sequence's length
+   * (rows beyond seqlen are not computed).  Masks and ALiBi positions count
+   * from each sequence's first token.  The values are read by the GPU and not
+   * checked: the caller guarantees them (the Python layer checks a host copy).
+   * No counterpart in the reference, whose kernels take one fixed shape. */
+  const int32_t* cu_seqlens;
+  /* With cu_seqlens: NULL, or a device int32[batch] permutation of 0..batch-1,
+   * the order in which the sequences' work is dispatched.  Longest first keeps
+   * the longest sequences off the end of the launch (the Python layer passes
+   * it).  Ignored without cu_seqlens; not checked on the GPU. */
+  const int32_t* seq_order;
+  int32_t reserved[2];        /* must be zero */
 } chia_attn_args;
 
 /* Launch one forward attention on `stream` (a hipStream_t; NULL = default
@@ -114,8 +132,9 @@ typedef struct chia_attn_args {
 int chia_attn_fwd(const chia_attn_args* args, void* stream);
 
 /* chia_attn_fwd that also writes, for a SOFTMAX normaliser, the log-sum-exp of
- * each row's modified, masked scores: lse[(b * H + h) * S + i] =
- * log(sum_j visible exp(s_ij)), fp32, -inf for a row that sees no key -- the
+ * each row's modified, masked scores: lse[(b * H + h) * S + i] (packed
+ * sequences: lse[t * H + h] for token t) = log(sum_j visible exp(s_ij)), fp32,
+ * -inf for a row that sees no key -- the
  * statistic chia_attn_bwd needs.  lse must be non-NULL (4-byte aligned) for
  * SOFTMAX and is ignored for SIGMOID / RELU.  No counterpart in the reference,
  * whose kernels are forward-only (README.md:223); this is the training

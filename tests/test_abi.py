@@ -83,7 +83,7 @@ def test_validation_codes(lib_built):
     assert _plan_status(heads=8, kv_heads=3) == -2
     assert _plan_status(heads=8, kv_heads=-1) == -2
     a = make_args(batch=1, heads=1, seqlen=128, head_dim=64)
-    a.reserved[3] = 1
+    a.reserved[1] = 1
     assert lib_built.chia_attn_plan(ctypes.byref(a), ctypes.byref(_lib.PlanInfo())) == -8
 
 
