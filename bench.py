@@ -286,6 +286,45 @@ def varlen_report(args) -> int:
     return 0
 
 
+def fp8_report(cases, inputs, works, args) -> int:
+    """Per variant: the FP8 forward (attention_fp8, e4m3 q / k / v quantised per
+    tensor from the suite's inputs) against the bf16 forward on the same inputs:
+    HIP-event median per call and algorithmic TFLOP/s (4 D per visible pair)."""
+    import torch
+
+    from chia_proj_amd import OPS, attention_fp8, core_kwargs, quantize_fp8
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS
+    from chia_proj_amd.timing import median_us
+
+    PEAK_FP8_TFLOPS = 2 * PEAK_BF16_TFLOPS
+    rows, tot_fp8, tot_bf16, tot_flops = {}, 0.0, 0.0, 0.0
+    for c in cases:
+        q, k, v, params = inputs[c.name]
+        kw = core_kwargs(c.op, c.H, **params)
+        (q8, qd), (k8, kd), (v8, vd) = (quantize_fp8(t) for t in (q, k, v))
+        us8 = median_us(lambda: attention_fp8(q8, k8, v8, q_descale=qd, k_descale=kd, v_descale=vd, **kw))
+        us16 = median_us(lambda: OPS[c.op](q, k, v, **params))
+        flops = works[c.name]["flops_alg"]
+        tf8, tf16 = flops / (us8 * 1e-6) / 1e12, flops / (us16 * 1e-6) / 1e12
+        rows[c.op] = {"fp8_us": round(us8, 2), "bf16_us": round(us16, 2), "fp8_tflops_alg": round(tf8, 2),
+                      "pct_fp8_peak": round(100 * tf8 / PEAK_FP8_TFLOPS, 2), "speedup": round(us16 / us8, 3)}
+        tot_fp8 += us8
+        tot_bf16 += us16
+        tot_flops += flops
+        log(f"  fp8 {c.op:22s} {us8:8.1f} us ({tf8:7.1f} TF/s, {100 * tf8 / PEAK_FP8_TFLOPS:5.1f}% of fp8 peak)"
+            f"   bf16 {us16:8.1f} us   x{us16 / us8:5.2f}")
+    c0 = cases[0]
+    print(json.dumps({
+        "metric": "fp8 forward (e4m3 q, k, v) algorithmic TFLOP/s over the ten variants",
+        "value": round(tot_flops / (tot_fp8 * 1e-6) / 1e12, 2), "unit": "TFLOP/s", "higher_is_better": True,
+        "dtype": "fp8_e4m3", "data": "synthetic", "n_gpus": 1,
+        "config": {"workload": f"ten variants, B{c0.B} H{c0.H} S{c0.S} D{c0.D}, e4m3 per-tensor scales",
+                   "suite": args.suite},
+        "bf16_same_step_us": round(tot_bf16, 2), "fp8_step_us": round(tot_fp8, 2), "variants": rows,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -306,6 +345,9 @@ def main() -> int:
     ap.add_argument("--varlen", action="store_true",
                     help="time a packed variable-length batch (attention_varlen) against padding and per-sequence "
                          "launches; prints its own JSON line")
+    ap.add_argument("--fp8", action="store_true",
+                    help="time the FP8 (e4m3) forward of each variant against the bf16 forward; prints its own "
+                         "JSON line")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
                          "kernel that reads and writes 512 MiB, and exit (with --backward: two backward passes per variant)")
@@ -348,6 +390,8 @@ def main() -> int:
         return backward_report(cases, inputs, works, args)
     if args.flex:
         return flex_report(cases, inputs, calls, args)
+    if args.fp8:
+        return fp8_report(cases, inputs, works, args)
     outputs = {c.name: calls[c.name]() for c in cases}
     torch.cuda.synchronize()
 

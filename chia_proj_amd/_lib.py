@@ -23,6 +23,7 @@ ABI_VERSION = 3
 EXPORTS = (
     "chia_attn_fwd",
     "chia_attn_fwd_lse",
+    "chia_attn_fwd_fp8",
     "chia_attn_bwd",
     "chia_attn_bwd_workspace_size",
     "chia_attn_plan",
@@ -108,6 +109,27 @@ class BwdArgs(ctypes.Structure):
             setattr(self, key, val)
 
 
+class Fp8Args(ctypes.Structure):
+    """Mirror of ``chia_attn_fp8_args``."""
+
+    _fields_ = [
+        ("struct_size", ctypes.c_uint32),
+        ("format", ctypes.c_uint32),
+        ("attn", ctypes.POINTER(AttnArgs)),
+        ("q_descale", ctypes.c_float),
+        ("k_descale", ctypes.c_float),
+        ("v_descale", ctypes.c_float),
+        ("reserved", ctypes.c_int32 * 5),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(Fp8Args)
+        self.q_descale = self.k_descale = self.v_descale = 1.0
+        for key, val in kw.items():
+            setattr(self, key, val)
+
+
 class PlanInfo(ctypes.Structure):
     """Mirror of ``chia_attn_plan_info``."""
 
@@ -157,6 +179,8 @@ def _load():
         lib.chia_attn_fwd.restype = ctypes.c_int
         lib.chia_attn_fwd_lse.argtypes = [ctypes.POINTER(AttnArgs), ctypes.c_void_p, ctypes.c_void_p]
         lib.chia_attn_fwd_lse.restype = ctypes.c_int
+        lib.chia_attn_fwd_fp8.argtypes = [ctypes.POINTER(Fp8Args), ctypes.c_void_p]
+        lib.chia_attn_fwd_fp8.restype = ctypes.c_int
         lib.chia_attn_bwd.argtypes = [ctypes.POINTER(BwdArgs), ctypes.c_void_p]
         lib.chia_attn_bwd.restype = ctypes.c_int
         lib.chia_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
@@ -202,6 +226,12 @@ def fwd_lse(args: AttnArgs, lse_ptr: int, stream: int) -> None:
     st = _load().chia_attn_fwd_lse(ctypes.byref(args), ctypes.c_void_p(lse_ptr), ctypes.c_void_p(stream))
     if st != 0:
         raise ChiaAttnError(st, "chia_attn_fwd_lse")
+
+
+def fwd_fp8(args: Fp8Args, stream: int) -> None:
+    st = _load().chia_attn_fwd_fp8(ctypes.byref(args), ctypes.c_void_p(stream))
+    if st != 0:
+        raise ChiaAttnError(st, "chia_attn_fwd_fp8")
 
 
 def bwd_workspace_size(args: AttnArgs) -> int:

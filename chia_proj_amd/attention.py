@@ -302,6 +302,80 @@ def run_backward(do, q, k, v, o, lse, params):
     return dq, dk, dv
 
 
+# ---- FP8 (e4m3) operands ----------------------------------------------------------
+
+FP8_DTYPE = torch.float8_e4m3fn
+FP8_MAX = 448.0
+
+
+def quantize_fp8(x: torch.Tensor, amax: Optional[float] = None):
+    """Per-tensor e4m3 quantisation: (x8, descale) with x ~= x8.float() * descale;
+    the scale maps max |x| (or `amax`) to 448, the e4m3 maximum."""
+    a = float(x.detach().abs().max()) if amax is None else float(amax)
+    descale = a / FP8_MAX if a > 0 and math.isfinite(a) else 1.0
+    x8 = (x.float() / descale).clamp(-FP8_MAX, FP8_MAX).to(FP8_DTYPE)
+    return x8, descale
+
+
+def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descale: float = 1.0,
+                  k_descale: float = 1.0, v_descale: float = 1.0, norm: str = "softmax", causal: bool = True,
+                  window: int = 0, dilation: int = 1, block: int = 0, prefix: int = 0,
+                  scale: Optional[float] = None, head_scale: PerHead = None, alibi_slopes: PerHead = None,
+                  softcap: float = 0.0, bias: float = 0.0, post_scale: float = 1.0,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """attention() on float8 e4m3 q, k, v ([B, H, S, D] / [B, H_kv, S, D]) with
+    per-tensor descales (real = stored * descale); returns bf16 o.  Both products
+    run on the gfx950 FP8 matrix path (chia_attn_fwd_fp8); the attention weights
+    are rounded to e4m3 (after scaling by 2^8).  Forward only."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dtype != FP8_DTYPE:
+            raise TypeError(f"{name} must be a torch.float8_e4m3fn tensor, got "
+                            f"{getattr(t, 'dtype', type(t).__name__)}")
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4-D, got shape {tuple(t.shape)}")
+    B, H, S, D = q.shape
+    if (k.shape != v.shape or k.shape[0] != B or k.shape[2:] != q.shape[2:] or k.shape[1] < 1
+            or H % k.shape[1] != 0):
+        raise ValueError(f"k and v must be [B, H_kv, S, D] with H_kv dividing q's H, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
+        raise ValueError("q, k, v must be on the same GPU device")
+    if min(B, H, S) < 1:
+        raise ValueError(f"empty tensor shape {tuple(q.shape)}")
+    for name, d in (("q_descale", q_descale), ("k_descale", k_descale), ("v_descale", v_descale)):
+        if not (float(d) > 0 and math.isfinite(float(d))):
+            raise ValueError(f"{name} must be finite and > 0, got {d}")
+    sc = _check_params(D, norm, window, dilation, block, prefix, scale, softcap)
+
+    def fp8_layout_ok(t):
+        return t.stride(-1) == 1 and all(s % 16 == 0 for s in t.stride()[:3]) and t.data_ptr() % 16 == 0
+
+    q_, k_, v_ = (t if fp8_layout_ok(t) else t.contiguous() for t in (q, k, v))
+    if out is None:
+        o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    else:
+        if out.shape != q.shape or out.dtype != torch.bfloat16 or out.device != q.device or not _layout_ok(out):
+            raise ValueError("out must be a bf16 tensor of q's shape on q's device with unit last stride")
+        o = out
+    hs = _per_head_vector(head_scale, H, q.device, "head_scale", positive=True)
+    sl = _per_head_vector(alibi_slopes, H, q.device, "alibi_slopes", positive=False)
+    a = make_args(batch=B, heads=H, seqlen=S, head_dim=D, norm=norm, causal=causal, window=window,
+                  dilation=dilation, block=block, prefix=prefix, scale=sc, softcap=softcap, bias=bias,
+                  post_scale=post_scale)
+    a.q, a.k, a.v, a.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
+    a.kv_heads = k_.shape[1] if k_.shape[1] != H else 0
+    for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = t.stride(0), t.stride(1), t.stride(2)
+    a.head_scale = hs.data_ptr() if hs is not None else None
+    a.alibi_slopes = sl.data_ptr() if sl is not None else None
+    f = _lib.Fp8Args(attn=ctypes.pointer(a), q_descale=float(q_descale), k_descale=float(k_descale),
+                     v_descale=float(v_descale))
+    with torch.cuda.device(q.device):
+        _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
+    return o
+
+
 # ---- packed variable-length batches -------------------------------------------
 
 def _layout_ok_packed(t: torch.Tensor) -> bool:

@@ -10,7 +10,7 @@
 #include <cmath>
 #include <cstring>
 
-#include "attn_bwd_kernel.h"
+#include "attn_fp8_kernel.h"
 #include "chia_attn.h"
 
 namespace chia {
@@ -20,6 +20,7 @@ KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
 KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d128(int norm, bool alibi, bool softcap);
+Fp8KernelFn select_fp8_kernel(int head_dim, int norm, bool alibi, bool softcap);
 
 namespace {
 
@@ -320,6 +321,61 @@ extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
   if (softmax) err = launch(ks.stats, g_stats, p, s);
   if (err == hipSuccess) err = launch(ks.dq, g_dq, p, s);
   if (err == hipSuccess) err = launch(ks.dkdv, g_dkdv, p, s);
+  return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
+}
+
+extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
+  if (!fa) return CHIA_ATTN_ERR_NULL;
+  if (fa->struct_size != sizeof(chia_attn_fp8_args) || fa->format != 0) return CHIA_ATTN_ERR_STRUCT;
+  for (int i = 0; i < 5; ++i)
+    if (fa->reserved[i] != 0) return CHIA_ATTN_ERR_STRUCT;
+  const chia_attn_args* a = fa->attn;
+  const int st = validate(a, true);
+  if (st != CHIA_ATTN_OK) return st;
+  if (a->cu_seqlens) return CHIA_ATTN_ERR_SHAPE;
+  for (float d : {fa->q_descale, fa->k_descale, fa->v_descale})
+    if (!(d > 0.f) || !std::isfinite(d)) return CHIA_ATTN_ERR_SCALE;
+  // fp8 rows are D bytes: the 16-byte DMA chunks need byte strides that are multiples of 16
+  for (const int64_t* s : {a->q_stride, a->k_stride, a->v_stride})
+    if (s[0] % 16 || s[1] % 16 || s[2] % 16) return CHIA_ATTN_ERR_ALIGN;
+  if (a->q_stride[2] * a->dilation >= kMaxKvRowStride) return CHIA_ATTN_ERR_SHAPE;
+
+  Fp8Params p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = (const uint8_t*)a->q;
+  p.k = (const uint8_t*)a->k;
+  p.v = (const uint8_t*)a->v;
+  p.o = (uint16_t*)a->o;
+  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
+  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
+  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
+  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.head_scale = a->head_scale;
+  p.alibi_slopes = a->alibi_slopes;
+  p.mask = spec_of(a);
+  p.B = (int32_t)a->batch;
+  p.H = (int32_t)a->heads;
+  p.residues = num_residues(p.mask);
+  p.n_blk = (residue_geom(p.mask, 0).S + 127) / 128;
+  const int64_t n_wg = a->batch * a->heads * p.residues * (int64_t)p.n_blk;
+  if (n_wg >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
+  p.n_wg = (int32_t)n_wg;
+  p.div_blk = make_udiv(p.n_blk);
+  p.div_res = make_udiv(p.residues);
+  p.div_h = make_udiv(p.H);
+  p.div_group = make_udiv(a->kv_heads > 0 ? (int32_t)(a->heads / a->kv_heads) : 1);
+  p.qk_scale = a->scale * fa->q_descale * fa->k_descale;
+  p.v_descale = fa->v_descale;
+  p.softcap = a->softcap;
+  p.bias = a->bias;
+  p.post_scale = a->post_scale;
+  const Fp8KernelFn fn = select_fp8_kernel((int)a->head_dim, (int)a->norm, a->alibi_slopes != nullptr, a->softcap > 0.f);
+  if (!fn) return CHIA_ATTN_ERR_NORM;
+  void* kargs[] = {&p};
+  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(256), kargs, 0,
+                                   (hipStream_t)stream);
+  if (err != hipSuccess) return (int)err;
+  err = hipGetLastError();
   return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
 }
 

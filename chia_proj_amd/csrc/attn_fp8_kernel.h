@@ -1,0 +1,341 @@
+// attn_fp8_kernel.h -- gfx950 forward attention with FP8 (OCP e4m3) operands.
+//
+// Semantics: the forward of attn_fwd_kernel.h (mask, score modifiers,
+// normalisers) for q, k, v stored as float8 e4m3 with per-tensor
+// dequantisation factors (real value = stored value * descale); o is bf16.
+// Both products run on v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales),
+// twice the bf16 matrix rate:
+//   S^T[key, query] = K Q^T   A = K rows (two ds_read_b128 per lane), B = Q
+//                             rows in VGPRs; both operands put the same 32
+//                             bytes of d in the same (lane half, byte) slots,
+//                             which is all the contraction needs;
+//   O^T[d, query] += V^T P^T  B = P^T: the lane's own 32 weights (lane =
+//                             query, keys 8w + 4h + {0..3} in dword w, h the
+//                             lane half), rounded to e4m3; A =
+//                             V^T gathered from the row-major V tile with
+//                             ds_read_b64_tr_b8 -- within a 16-lane group,
+//                             lane j + 8p receives byte j of the 8-byte
+//                             chunks read by lanes 2t + p (t = 0..7), so
+//                             pointing lane 2t + p at key 16 wp + 4h + (t & 3)
+//                             + 8 (t >> 2), columns d0 + 8p, hands lane j + 8p
+//                             the four-key groups of dwords 2 wp, 2 wp + 1 of
+//                             column d0 + 8p + j -- the keys of the B operand.
+// The row sum adds the unrounded fp32 weights.  Softmax weights are
+// 2^(x - m + 4) with a running max m that moves (rescaling O and l) only when
+// a tile's max exceeds it by more than 4 (log2): weights stay <= 2^8 < 448,
+// the e4m3 maximum, and weights down to 2^-13 of the row max stay normal.
+// Sigmoid weights are scaled by 2^8; ReLU weights are clamped to 448.  One workgroup = 4 wavefronts x 32 query rows; K and V tiles of 64 keys
+// are DMA'd HBM -> LDS (16-byte chunks XOR-swizzled by row) in three stages
+// with one barrier per tile, as in the bf16 kernels.
+#pragma once
+#include "attn_bwd_kernel.h"  // attn_fwd_kernel.h and zero_hidden
+
+namespace chia {
+
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
+
+constexpr int kFp8E4M3 = 0;  // MFMA operand format code (cbsz / blgp)
+constexpr float kFp8Max = 448.0f;
+// Softmax weights are 2^(x - m + kFp8Pre) with a running max m that moves
+// only when a tile's max exceeds it by more than kFp8Lazy: weights <= 2^8.
+constexpr float kFp8Pre = 4.0f;
+constexpr float kFp8Lazy = 4.0f;
+
+struct Fp8Params {
+  const uint8_t* q;
+  const uint8_t* k;
+  const uint8_t* v;
+  uint16_t* o;
+  int64_t q_sb, q_sh, q_ss;  // element (= byte) strides: batch, head, seq
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;  // bf16 element strides
+  const float* head_scale;
+  const float* alibi_slopes;
+  MaskSpec mask;
+  int32_t B, H, residues, n_blk, n_wg;
+  UDiv div_blk, div_res, div_h, div_group;
+  float qk_scale;   // scale * q_descale * k_descale
+  float v_descale;
+  float softcap, bias, post_scale;
+};
+
+// Swizzled 16-byte slot of chunk c of row r in an fp8 tile of D-byte rows.
+template <int D>
+__device__ __forceinline__ int fp8_slot(int r, int c) {
+  return c ^ (r & (D / 16 - 1));
+}
+
+// One 64-row fp8 tile (row stride rs bytes, rows from `row`, clamped to
+// S - 1) into LDS at dst with the swizzle above; wavefront w of 4 moves
+// chunks [(n 4 + w) 64, +64) for n < NDMA.
+template <int D>
+__device__ __forceinline__ void fp8_dma_rows(const uint8_t* base, int64_t rs, int row, int S, char* dst, int wave,
+                                             int lane) {
+  constexpr int DQ = D / 16;
+  constexpr int NDMA = 64 * DQ / 256;
+  const uint8_t* src = base + (int64_t)row * rs;
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int pos = (n * 4 + wave) * 64 + lane;
+    const int r = pos / DQ, slot = pos % DQ;
+    const int rr = imin32(r, S - 1 - row);
+    dma16s(src, (uint32_t)((int64_t)rr * rs + 16 * fp8_slot<D>(r, slot)), lds_addr(dst + (n * 4 + wave) * 1024));
+  }
+}
+
+// Two e4m3 weights into bytes (2 HI, 2 HI + 1) of `old` (round to nearest even).
+template <bool HI>
+__device__ __forceinline__ int pk_fp8(float a, float b, int old) {
+  return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, HI);
+}
+
+template <int D, int NORM, bool ALIBI, bool SOFTCAP>
+__global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p) {
+  constexpr int NW = 4, BN = 64, KB = 2;
+  constexpr int RP = D;                 // LDS row pitch (bytes)
+  constexpr int T_BYTES = BN * RP;
+  constexpr int STAGE_BYTES = 2 * T_BYTES;
+  constexpr int NS = 3;
+  constexpr int KC = D / 64;            // 64-deep steps of the QK^T MFMA
+  constexpr int DB = D / 32;            // 32-row d blocks of O^T
+  constexpr int NDMA2 = 2 * (BN * (D / 16) / 256);  // DMA loads per tile per wavefront (K and V)
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, lh = lane >> 5;
+
+  // workgroup -> (b, h, residue, 128-row block), the blocks with the most keys first
+  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  const int bhr = udiv(L, p.div_blk);
+  const int blk = p.n_blk - 1 - (L - bhr * p.n_blk);
+  const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
+  const int b = udiv(bh, p.div_h), h = bh - b * p.H;
+  const MaskGeom g = residue_geom(p.mask, r);
+  const int nblk_r = (g.S + 127) / 128;
+  if (blk >= nblk_r) return;  // whole workgroup, before any barrier
+  const int dil = p.mask.dil;
+  const int hk = udiv(h, p.div_group);
+  const uint8_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
+  const uint8_t* kh = p.k + b * p.k_sb + hk * p.k_sh + r * p.k_ss;
+  const uint8_t* vh = p.v + b * p.v_sb + hk * p.v_sh + r * p.v_ss;
+  uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + r * p.o_ss;
+  const int64_t qrs = p.q_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil, ors = p.o_ss * dil;
+
+  // per-head score constants: x = log2-domain score (softmax) or the score itself
+  const float c1 = p.qk_scale * (p.head_scale ? p.head_scale[h] : 1.0f);
+  const float sl = (ALIBI && p.alibi_slopes) ? p.alibi_slopes[h] * (float)dil : 0.0f;
+
+  // this wavefront's 32 rows: Q as the MFMA B operand (lane = row, 32 bytes of d per 64)
+  const int row0 = blk * 128 + 32 * wave;
+  const int i = row0 + lq;
+  const bool ok = i < g.S;
+  i32x8_t qf[KC];
+  {
+    const uint8_t* qs = qh + (int64_t)(ok ? i : 0) * qrs + 32 * lh;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const u32x4_t lo = *(const u32x4_t*)(qs + 64 * kc);
+      const u32x4_t hi = *(const u32x4_t*)(qs + 64 * kc + 16);
+      qf[kc] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+  }
+
+  const int wg_hi = imin32(blk * 128 + 127, g.S - 1);
+  const TileRange tr = tile_range(g, blk * 128, wg_hi, BN);
+  const int ntiles = tr.n_pre + tr.n2;
+  const bool wvalid = row0 < g.S;
+  const int ra = row0, rb = imin32(row0 + 31, g.S - 1);
+
+  f32x16_t oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // LDS lane offsets.  K rows (A operand of S^T): row 32 kb + lq, chunks 4 kc + 2 lh (+1).
+  // V^T (A operand of O^T) by transposed reads: lane q of 16-lane group G reads key
+  // 16 wp + 4 hh + (t & 3) + 8 (t >> 2) (t = q / 2), columns 32 db + 16 (G & 1) + 8 (q & 1).
+  const int grp = lane >> 4, q16 = lane & 15;
+  const int t_src = q16 >> 1, p_src = q16 & 1, hh = grp >> 1;
+  const int v_key = 4 * hh + (t_src & 3) + 8 * (t_src >> 2);  // + 16 wp
+
+  auto issue = [&](int it) {
+    const int jt0 = tile_at(tr, it) * BN;
+    char* st = lds + (it % NS) * STAGE_BYTES;
+    fp8_dma_rows<D>(kh, krs, jt0, g.S, st, wave, lane);
+    fp8_dma_rows<D>(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
+  };
+  int dma_next = 0;
+  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+
+  for (int it = 0; it < ntiles; ++it) {
+    if (dma_next - (it + 1) >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA2) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (dma_next < ntiles) issue(dma_next++);
+    const char* St = lds + (it % NS) * STAGE_BYTES;
+    const int jt0 = tile_at(tr, it) * BN;
+    const int cls = wvalid ? classify_tile(g, ra, rb, jt0, jt0 + BN - 1) : (int)TILE_EMPTY;
+    if (cls == TILE_EMPTY) continue;
+
+    // S^T for the tile's two 32-key blocks
+    f32x16_t sacc[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
+      const int kr = 32 * kb + lq;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const int c0 = 4 * kc + 2 * lh;
+        const u32x4_t lo = *(const u32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0));
+        const u32x4_t hi = *(const u32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0 + 1));
+        const i32x8_t a = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        sacc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qf[kc], sacc[kb], kFp8E4M3, kFp8E4M3, 0,
+                                                                  0x7f7f7f7f, 0, 0x7f7f7f7f);
+      }
+    }
+
+    // scores -> weights (lane = query i; register e of block kb = key jt0 + 32 kb + 8 (e >> 2) + (e & 3) + 4 lh).
+    // Without ALiBi / softcap the score's scale folds into the weight's first operation.
+    constexpr bool kPlain = !ALIBI && !SOFTCAP;
+    float x[KB][16];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        if constexpr (kPlain) {
+          x[kb][e] = sacc[kb][e];
+        } else {
+          float u = sacc[kb][e] * c1;
+          if constexpr (ALIBI) u = __builtin_fmaf(sl, (float)(jt0 + 32 * kb + 8 * (e >> 2) + (e & 3) + 4 * lh - i), u);
+          if constexpr (SOFTCAP) {
+            const float th =
+                1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * (2.0f * kLog2e / p.softcap)));
+            u = p.softcap * th;
+          }
+          x[kb][e] = u;
+        }
+      }
+    uint32_t hidden[KB] = {0u, 0u};
+    if (cls == TILE_PARTIAL) {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) hidden[kb] = hidden_bits(g, i, jt0 + 32 * kb + 4 * lh);
+    }
+    float pw[KB][16];
+    if constexpr (NORM == NORM_SOFTMAX) {
+      // working units: raw scores (plain, scaled by kq = c1 log2 e in the exponent) or log2 units
+      const float kq = c1 * kLog2e;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float xv = kPlain ? x[kb][e] : x[kb][e] * kLog2e;
+          if (cls == TILE_PARTIAL && ((hidden[kb] >> (8 * (e >> 2) + (e & 3))) & 1u)) xv = -INFINITY;
+          x[kb][e] = xv;
+          mx = fmaxf(mx, xv);
+        }
+      mx = xhalf_max(mx);
+      const float ml2 = kPlain ? mx * kq : mx;  // kq > 0 keeps the order; -inf stays -inf
+      const float m_new = ml2 > m_run + kFp8Lazy ? ml2 : m_run;
+      if (__any(m_new != m_run)) {
+        const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) oacc[db][e] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = (m_run == -INFINITY) ? 0.f : m_run - kFp8Pre;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          pw[kb][e] = __builtin_amdgcn_exp2f(kPlain ? __builtin_fmaf(x[kb][e], kq, -m_use) : x[kb][e] - m_use);
+          l_run += pw[kb][e];
+        }
+    } else {
+      // sigmoid: 2^8 / (1 + 2^(-(t + bias) log2 e)) = rcp(2^-8 e + 2^-8); ReLU: clamp(t, 0, 448)
+      const float nk = kPlain ? -c1 * kLog2e : -kLog2e, nb = -p.bias * kLog2e;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float w;
+          if constexpr (NORM == NORM_SIGMOID) {
+            const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kb][e], nk, nb));
+            w = __builtin_amdgcn_rcpf(__builtin_fmaf(ex, 1.0f / 256.0f, 1.0f / 256.0f));
+          } else {
+            const float t = kPlain ? x[kb][e] * c1 : x[kb][e];
+            w = __builtin_amdgcn_fmed3f(t, 0.0f, kFp8Max);
+          }
+          pw[kb][e] = w;
+        }
+        if (cls == TILE_PARTIAL) zero_hidden(pw[kb], hidden[kb]);
+      }
+    }
+
+    // P^T as the B operand: dword w = 4 kb + (e >> 2) holds keys 8 w + 4 lh + (e & 3)
+    i32x8_t pb;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const int kb = w >> 2, e0 = 4 * (w & 3);
+      int d = pk_fp8<false>(pw[kb][e0], pw[kb][e0 + 1], 0);
+      d = pk_fp8<true>(pw[kb][e0 + 2], pw[kb][e0 + 3], d);
+      pb[w] = d;
+    }
+
+    // O^T += V^T P^T, one MFMA per 32-row d block
+    const char* Vt = St + T_BYTES;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int chunk = 2 * db + (grp & 1);
+      i32x8_t va;
+#pragma unroll
+      for (int wp = 0; wp < 4; ++wp) {
+        const int key = 16 * wp + v_key;
+        const char* src = Vt + key * RP + 16 * fp8_slot<D>(key, chunk) + 8 * p_src;
+        const i32x2_t t2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)src);
+        va[2 * wp] = t2[0];
+        va[2 * wp + 1] = t2[1];
+      }
+      oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, pb, oacc[db], kFp8E4M3, kFp8E4M3, 0, 0x7f7f7f7f,
+                                                                 0, 0x7f7f7f7f);
+    }
+  }
+
+  // epilogue: o = O^T^T * v_descale / (2^8 l) (softmax) or * v_descale * post / 2^8
+  if (ok) {
+    float f;
+    if constexpr (NORM == NORM_SOFTMAX) {
+      const float lt = xhalf_sum(l_run);
+      f = lt > 0.f ? p.v_descale / lt : 0.f;
+    } else if constexpr (NORM == NORM_SIGMOID) {
+      f = p.v_descale * p.post_scale * (1.0f / 256.0f);
+    } else {
+      f = p.v_descale * p.post_scale;
+    }
+    uint16_t* dst = oh + (int64_t)i * ors + 4 * lh;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2_t w;
+        w[0] = pack_bf16x2(oacc[db][4 * gq + 0] * f, oacc[db][4 * gq + 1] * f);
+        w[1] = pack_bf16x2(oacc[db][4 * gq + 2] * f, oacc[db][4 * gq + 3] * f);
+        *(u32x2_t*)(dst + 32 * db + 8 * gq) = w;
+      }
+  }  // (lanes l and l + 32 hold the same row, so the half-wave sum above runs on both or neither)
+}
+
+using Fp8KernelFn = void (*)(Fp8Params);
+
+}  // namespace chia

@@ -174,6 +174,24 @@ int64_t chia_attn_bwd_workspace_size(const chia_attn_args* fwd);
  * buffer alive until it completes).  Status codes as chia_attn_fwd. */
 int chia_attn_bwd(const chia_attn_bwd_args* args, void* stream);
 
+/* FP8 forward.  `attn` describes the call as for chia_attn_fwd, with q, k, v
+ * pointing at float8 e4m3 data (OCP e4m3fn: 4 exponent bits, bias 7, max 448;
+ * strides in elements = bytes, multiples of 16; 16-byte aligned) and o at
+ * bf16 [B, H, S, D].  Real values are stored values times the descales.  Both
+ * products run on the gfx950 FP8 matrix path (twice the bf16 rate): the
+ * weights are rounded to e4m3 after scaling by 2^8, the accumulation is fp32;
+ * ReLU weights above 448 saturate.  cu_seqlens is not supported (NULL).  No
+ * counterpart in the reference, whose kernels are bf16 only. */
+typedef struct chia_attn_fp8_args {
+  uint32_t struct_size;        /* sizeof(chia_attn_fp8_args) */
+  uint32_t format;             /* 0 = e4m3 for q, k and v (the only format) */
+  const chia_attn_args* attn;  /* shapes, strides, mask, score, normaliser; q, k, v fp8; o bf16 */
+  float q_descale, k_descale, v_descale;  /* > 0, finite */
+  int32_t reserved[5];         /* must be zero */
+} chia_attn_fp8_args;
+
+int chia_attn_fwd_fp8(const chia_attn_fp8_args* args, void* stream);
+
 /* Host-only schedule statistics for `args` (no GPU call).  Used by the
  * benchmark's FLOP accounting; the reference has no counterpart (its timer,
  * extra_bench.py:8-22, counts latency only). */

@@ -21,7 +21,7 @@ HEADER = Path(__file__).resolve().parent.parent / "include" / "chia_attn.h"
 
 def test_library_exports_every_declared_symbol(lib_built):
     text = HEADER.read_text()
-    declared = set(re.findall(r"\b(chia_attn_[a-z_]+)\s*\(", text))
+    declared = set(re.findall(r"\b(chia_attn_[a-z0-9_]+)\s*\(", text))
     assert declared == set(_lib.EXPORTS)
     for name in declared:
         assert hasattr(lib_built, name), name
@@ -43,7 +43,7 @@ def _c_struct_fields(text, name):
 
 
 @pytest.mark.parametrize("cname,pyclass", [("chia_attn_args", _lib.AttnArgs), ("chia_attn_plan_info", _lib.PlanInfo),
-                                           ("chia_attn_bwd_args", _lib.BwdArgs)])
+                                           ("chia_attn_bwd_args", _lib.BwdArgs), ("chia_attn_fp8_args", _lib.Fp8Args)])
 def test_ctypes_mirrors_header_struct(cname, pyclass):
     fields = _c_struct_fields(HEADER.read_text(), cname)
     assert fields == [f[0] for f in pyclass._fields_]
@@ -225,3 +225,30 @@ def test_bwd_rejects_bad_arguments_without_launching(lib_built):
     assert _bwd_status(c, lse=None, workspace=None, workspace_bytes=0, dq=None) == -1
     d = _bwd_ready_args(heads=512, kv_heads=1)       # more than 256 query heads per K/V head
     assert _bwd_status(d) == -2
+
+
+def test_fp8_rejects_bad_arguments_without_launching(lib_built):
+    a = make_args(batch=1, heads=1, seqlen=64, head_dim=64)
+    a.q = a.k = a.v = a.o = 0x1000
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = 64 * 64, 64 * 64, 64
+    f = _lib.Fp8Args(attn=ctypes.pointer(a))
+    call = lambda: lib_built.chia_attn_fwd_fp8(ctypes.byref(f), None)  # noqa: E731
+    assert lib_built.chia_attn_fwd_fp8(None, None) == -1
+    f.format = 1
+    assert call() == -8                      # only e4m3
+    f.format = 0
+    f.reserved[4] = 1
+    assert call() == -8
+    f.reserved[4] = 0
+    f.v_descale = 0.0
+    assert call() == -5
+    f.v_descale = float("inf")
+    assert call() == -5
+    f.v_descale = 1.0
+    a.q_stride[2] = 72                       # a multiple of 8 elements, not of 16 bytes
+    assert call() == -7
+    a.q_stride[2] = 64
+    a.cu_seqlens = 0x2000                    # packed sequences: not on the fp8 path
+    assert call() == -2

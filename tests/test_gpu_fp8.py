@@ -1,0 +1,95 @@
+"""GPU parity of the FP8 forward (chia_attn_fwd_fp8 through attention_fp8).
+
+Reference: attention of the dequantised e4m3 inputs (oracle/fp8.py::fp8_ref,
+fp32).  Gate (per (b, h) slice, relative to s = max(1, max |ref|)): the
+kernel's error may exceed twice the error of the FP8 rounding model
+(oracle/fp8.py::fp8_emulated: the weights rounded to e4m3 after scaling by
+2^8) by at most the bf16 gate -- max 2e-2 s, mean 2e-3 s.  FP8 is the gate
+"widened accordingly": the widening is measured, not chosen."""
+import pytest
+import torch
+
+from chia_proj_amd import OPS, attention_fp8, core_kwargs, quantize_fp8
+from oracle.fp8 import fp8_emulated, fp8_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+def _inputs(B, H, Hkv, S, D, seed):
+    g = torch.Generator("cpu").manual_seed(seed)
+    q = torch.randn(B, H, S, D, generator=g)
+    k, v = (torch.randn(B, Hkv, S, D, generator=g) for _ in range(2))
+    return [quantize_fp8(t) for t in (q, k, v)]
+
+
+def _check(name, qkv, kw):
+    (q8, qd), (k8, kd), (v8, vd) = qkv
+    o = attention_fp8(q8.to(DEV), k8.to(DEV), v8.to(DEV), q_descale=qd, k_descale=kd, v_descale=vd, **kw)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.bfloat16 and o.shape == q8.shape
+    ref = fp8_ref(q8, k8, v8, qd, kd, vd, **kw)
+    emu = fp8_emulated(q8, k8, v8, qd, kd, vd, **kw)
+    got = o.float().cpu()
+    assert torch.isfinite(got).all(), name
+    for b in range(ref.shape[0]):
+        for h in range(ref.shape[1]):
+            r = ref[b, h]
+            s = max(1.0, r.abs().max().item())
+            e_k = (got[b, h] - r).abs()
+            e_m = (emu[b, h] - r).abs()
+            assert e_k.max().item() <= 2 * e_m.max().item() + 2e-2 * s, (name, b, h, e_k.max().item(), e_m.max().item())
+            assert e_k.mean().item() <= 2 * e_m.mean().item() + 2e-3 * s, (name, b, h, e_k.mean().item(),
+                                                                           e_m.mean().item())
+    return o
+
+
+def _variant_kwargs(op, H):
+    kw = core_kwargs(op, H)
+    for key in ("head_scale", "alibi_slopes"):
+        if isinstance(kw.get(key), torch.Tensor):
+            kw[key] = kw[key].tolist()
+    return kw
+
+
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("D", [64, 128])
+def test_variants_reference_defaults(op, D):
+    _say(f"[fp8] {op} D={D}")
+    kw = _variant_kwargs(op, 4)
+    _check(f"{op} D={D}", _inputs(1, 4, 4, 600, D, 3000 + D), kw)
+
+
+EDGE = [
+    ("S1_causal", 1, 2, 2, 1, 64, dict(causal=True)),
+    ("S65_full", 2, 2, 2, 65, 64, dict(causal=False)),
+    ("S200_window33_dil3", 1, 2, 2, 200, 64, dict(causal=True, window=33, dilation=3)),
+    ("S777_block100_d128", 1, 2, 2, 777, 128, dict(causal=True, block=100)),
+    ("S600_prefix130", 1, 2, 2, 600, 64, dict(causal=True, prefix=130)),
+    ("S512_alibi_softcap", 1, 2, 2, 512, 64, dict(causal=True, alibi_slopes=[0.5, 0.125], softcap=20.0)),
+    ("gqa_headscale", 1, 4, 2, 300, 64, dict(causal=True, head_scale=[0.5, 1.0, 1.5, 2.0])),
+    ("mqa_sigmoid_local", 2, 4, 1, 257, 128, dict(norm="sigmoid", causal=False, window=64, bias=-3.0)),
+    ("relu_post_noncausal", 1, 2, 2, 333, 64, dict(norm="relu", causal=False, post_scale=0.01)),
+]
+
+
+@pytest.mark.parametrize("name,B,H,Hkv,S,D,kw", EDGE, ids=[e[0] for e in EDGE])
+def test_edge_cases(name, B, H, Hkv, S, D, kw):
+    _say(f"[fp8] edge {name}")
+    _check(name, _inputs(B, H, Hkv, S, D, S * 7 + D), kw)
+
+
+def test_deterministic_and_close_to_bf16():
+    """Two calls give the same bits; the FP8 output is within the FP8 gate of the
+    bf16 kernel run on the dequantised inputs."""
+    _say("[fp8] determinism")
+    qkv = _inputs(2, 4, 4, 1000, 64, 5)
+    a = _check("det", qkv, dict(causal=True, window=300))
+    (q8, qd), (k8, kd), (v8, vd) = qkv
+    b = attention_fp8(q8.to(DEV), k8.to(DEV), v8.to(DEV), q_descale=qd, k_descale=kd, v_descale=vd, causal=True,
+                      window=300)
+    assert torch.equal(a, b)
