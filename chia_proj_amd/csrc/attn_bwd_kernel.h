@@ -78,8 +78,10 @@ struct BwdParams {
 };
 
 // Per-score gradient (see the header): from the raw s = q.k, dp = do.v and
-// j - i, the probability p (for dV) and ds / c1 (for dQ, dK: the caller
-// applies c1, once per accumulated gradient where it is uniform).
+// j - i, the probability p (for dV) and ds (for dQ, dK).  Softmax: delta is
+// the row statistic delta c1, so ds = p (dp c1 - delta c1) includes c1; sigmoid
+// / ReLU: ds / c1, and the caller applies c1 (once per accumulated gradient
+// where it is uniform).
 template <int NORM, bool ALIBI, bool SOFTCAP>
 struct ScoreGrad {
   float c1, c1l2, sl, cap, k2cap, post, nbias_l2;
@@ -90,7 +92,7 @@ struct ScoreGrad {
       // t = s c1: the scale folds into one fma ahead of the exponential
       if constexpr (NORM == NORM_SOFTMAX) {
         p = __builtin_amdgcn_exp2f(__builtin_fmaf(s, c1l2, -lse2));
-        ds = p * (dp - delta);
+        ds = p * __builtin_fmaf(dp, c1, -delta);  // delta: the row's delta c1
       } else if constexpr (NORM == NORM_SIGMOID) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(s, -c1l2, nbias_l2)));
         p = post * sg;
@@ -113,7 +115,7 @@ struct ScoreGrad {
       float dt;
       if constexpr (NORM == NORM_SOFTMAX) {
         p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, kLog2e, -lse2));
-        dt = p * (dp - delta);
+        dt = p * __builtin_fmaf(dp, c1, -delta);
       } else if constexpr (NORM == NORM_SIGMOID) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(-t, kLog2e, nbias_l2)));
         p = post * sg;
@@ -213,7 +215,8 @@ __global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdParams p) 
   const int64_t o2 = ((int64_t)bh * p.residues + r) * p.SR + ir;
   const int64_t plane = (int64_t)p.B * p.H * p.residues * p.SR;
   p.stats[o2] = p.lse[b * p.lse_sb + h * p.lse_sh + t * p.lse_ss] * kLog2e;
-  p.stats[plane + o2] = acc;
+  // delta times the head's score scale c1: ds = p (dp c1 - delta c1) is then one fma and a multiply
+  p.stats[plane + o2] = acc * (p.scale * (p.head_scale ? p.head_scale[h] : 1.0f));
 }
 
 // ---- dQ ------------------------------------------------------------------------
@@ -359,7 +362,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   }
 
   if (ok) {
-    const float c1 = sg.c1;  // ds was accumulated without the head's scale
+    // sigmoid / ReLU ds was accumulated without the head's scale (softmax's includes it)
+    const float c1 = NORM == NORM_SOFTMAX ? 1.0f : sg.c1;
     uint16_t* dst = dqh + (int64_t)i * dqrs + 4 * lh;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -459,20 +463,43 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
   const int t_row = 4 * (g16 >> 1) + (s16 >> 2);
   const int t_lane = t_row * RP + 16 * ((2 * (g16 & 1) + ((s16 & 3) >> 1)) ^ t_row) + 8 * (s16 & 1);
 
-  auto tile_head = [&](int it) { return hkv * p.G + it / imax32(n_qt, 1); };
-  auto tile_row = [&](int it) { return (t_lo + it % imax32(n_qt, 1)) * BM; };
+  // Tiles run row tile t_lo .. t_lo + n_qt - 1 of query head hkv G, then of the
+  // next head of the group.  Two cursors walk them (the DMA one runs ahead);
+  // a head's base pointers are advanced only when the head changes.
+  struct Cursor {
+    int qt, hq;
+    const uint16_t* qb;
+    const uint16_t* dob;
+    const float* sb;
+  };
+  auto cursor0 = [&]() {
+    const int hq = hkv * p.G;
+    return Cursor{t_lo, hq, p.q + b * p.q_sb + hq * p.q_sh + t0 * p.q_ss,
+                  p.dout + b * p.do_sb + hq * p.do_sh + t0 * p.do_ss,
+                  p.stats + ((int64_t)(b * p.H + hq) * p.residues + r) * p.SR};
+  };
+  auto advance = [&](Cursor& c) {
+    if (++c.qt == t_lo + n_qt) {
+      c.qt = t_lo;
+      ++c.hq;
+      c.qb += p.q_sh;
+      c.dob += p.do_sh;
+      c.sb += (int64_t)p.residues * p.SR;
+    }
+  };
+  Cursor dc = cursor0(), cc = cursor0();
   auto issue = [&](int it) {
-    const int hq = tile_head(it), i0 = tile_row(it);
+    const int i0 = dc.qt * BM;
     char* st = lds + (it % NS) * STAGE_BYTES;
-    dma_rows<D, NW>(p.q + b * p.q_sb + hq * p.q_sh + t0 * p.q_ss, qrs, i0, g.S, st, wave, lane);
-    dma_rows<D, NW>(p.dout + b * p.do_sb + hq * p.do_sh + t0 * p.do_ss, dors, i0, g.S, st + T_BYTES, wave, lane);
+    dma_rows<D, NW>(dc.qb, qrs, i0, g.S, st, wave, lane);
+    dma_rows<D, NW>(dc.dob, dors, i0, g.S, st + T_BYTES, wave, lane);
     if constexpr (kStats) {
       // wavefront w moves 32 floats: lse log2 e rows [32 w, +32) (w < 2), or
       // delta rows [32 (w - 2), +32); the stats rows are padded to 64
-      const float* src = p.stats + (wave >= 2 ? plane : 0) + ((int64_t)(b * p.H + hq) * p.residues + r) * p.SR + i0 +
-                         32 * (wave & 1);
+      const float* src = dc.sb + (wave >= 2 ? plane : 0) + i0 + 32 * (wave & 1);
       if (lane < 32) dma4s(src, (uint32_t)(4 * lane), lds_addr(st + 2 * T_BYTES + 128 * wave));
     }
+    advance(dc);
   };
   constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64)) + (kStats ? 1 : 0);
   int dma_next = 0;
@@ -486,7 +513,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     asm volatile("" ::: "memory");
     if (dma_next < ntiles) issue(dma_next++);
     const char* St = lds + (it % NS) * STAGE_BYTES;
-    const int hq = tile_head(it), i0 = tile_row(it);
+    const int hq = cc.hq, i0 = cc.qt * BM;
+    advance(cc);
     // rows past the end of the sub-sequence are clamped copies: mask them
     int cls = wvalid ? classify_tile(g, i0, imin32(i0 + BM - 1, g.S - 1), kc, kd) : (int)TILE_EMPTY;
     if (cls == TILE_EMPTY) continue;
@@ -524,7 +552,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
         const float ls = NORM == NORM_SOFTMAX ? l4[e >> 2][e & 3] : 0.f;
         const float dl = NORM == NORM_SOFTMAX ? d4[e >> 2][e & 3] : 0.f;
         sg(sacc[e], pacc[e], (float)(j - (ibase + rc)), ls, dl, pv[e], dsv[e]);
-        dsv[e] *= sg.c1;  // the group's query heads may have different scales
+        if constexpr (NORM != NORM_SOFTMAX) dsv[e] *= sg.c1;  // the group's heads may differ in scale
       }
       if (cls == TILE_PARTIAL) {
         // bit k: row ibase + k does not see key j
