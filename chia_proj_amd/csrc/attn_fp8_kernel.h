@@ -33,6 +33,7 @@
 namespace chia {
 
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
 
@@ -138,9 +139,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     const uint8_t* qs = qh + (int64_t)(ok ? i : 0) * qrs + 32 * lh;
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
-      const u32x4_t lo = *(const u32x4_t*)(qs + 64 * kc);
-      const u32x4_t hi = *(const u32x4_t*)(qs + 64 * kc + 16);
-      qf[kc] = i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      const i32x4_t lo = *(const i32x4_t*)(qs + 64 * kc);
+      const i32x4_t hi = *(const i32x4_t*)(qs + 64 * kc + 16);
+      qf[kc] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     }
   }
 
@@ -194,9 +195,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
         const int c0 = 4 * kc + 2 * lh;
-        const u32x4_t lo = *(const u32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0));
-        const u32x4_t hi = *(const u32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0 + 1));
-        const i32x8_t a = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        const i32x4_t lo = *(const i32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0));
+        const i32x4_t hi = *(const i32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0 + 1));
+        const i32x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
         sacc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qf[kc], sacc[kb], kFp8E4M3, kFp8E4M3, 0,
                                                                   0x7f7f7f7f, 0, 0x7f7f7f7f);
       }
@@ -205,24 +206,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     // scores -> weights (lane = query i; register e of block kb = key jt0 + 32 kb + 8 (e >> 2) + (e & 3) + 4 lh).
     // Without ALiBi / softcap the score's scale folds into the weight's first operation.
     constexpr bool kPlain = !ALIBI && !SOFTCAP;
+    // x: the score in log2 units for softmax (osc = log2 e), in natural units otherwise.
+    //   no softcap: x = osc (c1 s + sl (j - i)) = fma(s, c1 osc, fma(sl osc, rc, base_kb))
+    //   softcap:    x = osc cap tanh(u / cap) = fma(r, -2 cap osc, cap osc), r = 1 / (1 + 2^(2 u log2e / cap))
+    // with rc = 8 (e >> 2) + (e & 3) the register's key offset and base_kb the block's first (j - i).
+    constexpr float osc = NORM == NORM_SOFTMAX ? kLog2e : 1.0f;
     float x[KB][16];
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
+    for (int kb = 0; kb < KB; ++kb) {
+      if constexpr (kPlain) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        if constexpr (kPlain) {
-          x[kb][e] = sacc[kb][e];
-        } else {
-          float u = sacc[kb][e] * c1;
-          if constexpr (ALIBI) u = __builtin_fmaf(sl, (float)(jt0 + 32 * kb + 8 * (e >> 2) + (e & 3) + 4 * lh - i), u);
+        for (int e = 0; e < 16; ++e) x[kb][e] = sacc[kb][e];
+      } else {
+        const float lk = SOFTCAP ? 2.0f * kLog2e / p.softcap : osc;  // units of the linear part
+        const float kql = c1 * lk, ksl = sl * lk;
+        const float base = ALIBI ? ksl * (float)(jt0 + 32 * kb + 4 * lh - i) : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float rc = (float)(8 * (e >> 2) + (e & 3));
+          const float lin = ALIBI ? __builtin_fmaf(sacc[kb][e], kql, __builtin_fmaf(ksl, rc, base)) : sacc[kb][e] * kql;
           if constexpr (SOFTCAP) {
-            const float th =
-                1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * (2.0f * kLog2e / p.softcap)));
-            u = p.softcap * th;
+            const float rr = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(lin));
+            // softmax keeps r: the max is a min over r and the affine map folds into the exponent
+            x[kb][e] = NORM == NORM_SOFTMAX ? rr : __builtin_fmaf(rr, -2.0f * p.softcap * osc, p.softcap * osc);
+          } else {
+            x[kb][e] = lin;
           }
-          x[kb][e] = u;
         }
       }
+    }
     uint32_t hidden[KB] = {0u, 0u};
     if (cls == TILE_PARTIAL) {
 #pragma unroll
@@ -232,17 +244,38 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     if constexpr (NORM == NORM_SOFTMAX) {
       // working units: raw scores (plain, scaled by kq = c1 log2 e in the exponent) or log2 units
       const float kq = c1 * kLog2e;
-      float mx = -INFINITY;
+      // softcap: x holds r, and the score is cA r + cB (cA < 0)
+      const float cA = -2.0f * p.softcap * kLog2e, cB = p.softcap * kLog2e;
+      if (cls == TILE_PARTIAL) {
+        // hidden keys -> -inf (r: +inf): all ones where hidden (v_bfe_i32), then one bitwise blend
+        uint32_t ninf;
+        asm("s_mov_b32 %0, %1" : "=s"(ninf) : "i"(SOFTCAP ? 0x7f800000 : 0xff800000));
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float xv = kPlain ? x[kb][e] : x[kb][e] * kLog2e;
-          if (cls == TILE_PARTIAL && ((hidden[kb] >> (8 * (e >> 2) + (e & 3))) & 1u)) xv = -INFINITY;
-          x[kb][e] = xv;
-          mx = fmaxf(mx, xv);
-        }
-      mx = xhalf_max(mx);
+          for (int e = 0; e < 16; ++e) {
+            uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)hidden[kb], 8 * (e >> 2) + (e & 3), 1);
+            asm("" : "+v"(m));
+            x[kb][e] = __uint_as_float((m & ninf) | (~m & __float_as_uint(x[kb][e])));
+          }
+      }
+      float mx;
+      if constexpr (SOFTCAP) {
+        float mr = INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mr = fminf(mr, x[kb][e]);
+        mr = -xhalf_max(-mr);
+        mx = mr == INFINITY ? -INFINITY : __builtin_fmaf(mr, cA, cB);
+      } else {
+        mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) mx = fmaxf(mx, x[kb][e]);
+        mx = xhalf_max(mx);
+      }
       const float ml2 = kPlain ? mx * kq : mx;  // kq > 0 keeps the order; -inf stays -inf
       const float m_new = ml2 > m_run + kFp8Lazy ? ml2 : m_run;
       if (__any(m_new != m_run)) {
@@ -259,7 +292,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-          pw[kb][e] = __builtin_amdgcn_exp2f(kPlain ? __builtin_fmaf(x[kb][e], kq, -m_use) : x[kb][e] - m_use);
+          float arg;
+          if constexpr (kPlain) arg = __builtin_fmaf(x[kb][e], kq, -m_use);
+          else if constexpr (SOFTCAP) arg = __builtin_fmaf(x[kb][e], cA, cB - m_use);
+          else arg = x[kb][e] - m_use;
+          pw[kb][e] = __builtin_amdgcn_exp2f(arg);
           l_run += pw[kb][e];
         }
     } else {
@@ -298,15 +335,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const int chunk = 2 * db + (grp & 1);
-      i32x8_t va;
+      i32x2_t t2[4];
 #pragma unroll
       for (int wp = 0; wp < 4; ++wp) {
         const int key = 16 * wp + v_key;
         const char* src = Vt + key * RP + 16 * fp8_slot<D>(key, chunk) + 8 * p_src;
-        const i32x2_t t2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)src);
-        va[2 * wp] = t2[0];
-        va[2 * wp + 1] = t2[1];
+        t2[wp] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)src);
       }
+      const i32x8_t va = __builtin_shufflevector(__builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3),
+                                                 __builtin_shufflevector(t2[2], t2[3], 0, 1, 2, 3), 0, 1, 2, 3, 4, 5,
+                                                 6, 7);
       oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, pb, oacc[db], kFp8E4M3, kFp8E4M3, 0, 0x7f7f7f7f,
                                                                  0, 0x7f7f7f7f);
     }
