@@ -325,6 +325,37 @@ def fp8_report(cases, inputs, works, args) -> int:
     return 0
 
 
+def configs_report(args) -> int:
+    """Every BASELINE.json configuration on its own shape (workloads.baseline_configs): HIP-event
+    median per call, algorithmic TFLOP/s and % of the bf16 MFMA peak, and the HBM roofline."""
+    import torch
+
+    from chia_proj_amd import OPS
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, PEAK_HBM_GBPS, work
+    from chia_proj_amd.timing import median_us
+    from chia_proj_amd.workloads import baseline_configs, draw_inputs
+
+    rows = {}
+    for c in baseline_configs():
+        q, k, v, params = draw_inputs(c, "cuda")
+        fn = lambda: OPS[c.op](q, k, v, **params)  # noqa: E731
+        us = median_us(fn)
+        w = work(c.op, c.B, c.H, c.S, c.D, params)
+        tf = w["flops_alg"] / (us * 1e-6) / 1e12
+        gbps = w["bytes"] / (us * 1e-6) / 1e9
+        rows[c.name] = {"op": c.op, "shape": [c.B, c.H, c.S, c.D], "us": round(us, 2), "tflops_alg": round(tf, 2),
+                        "pct_mfma_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
+                        "pct_hbm_roofline": round(100 * gbps / PEAK_HBM_GBPS, 2)}
+        log(f"  {c.name:36s} {us:9.1f} us  {tf:7.1f} TF/s ({100 * tf / PEAK_BF16_TFLOPS:5.1f}% MFMA, "
+            f"{100 * gbps / PEAK_HBM_GBPS:5.1f}% HBM)")
+        del q, k, v
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "BASELINE.json configurations: us/call + TFLOP/s per configuration", "unit": "us",
+                      "higher_is_better": False, "dtype": "bf16", "data": "synthetic", "n_gpus": 1,
+                      "configs": rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -348,6 +379,8 @@ def main() -> int:
     ap.add_argument("--fp8", action="store_true",
                     help="time the FP8 (e4m3) forward of each variant against the bf16 forward; prints its own "
                          "JSON line")
+    ap.add_argument("--configs", action="store_true",
+                    help="time every BASELINE.json configuration on its own shape; prints its own JSON line")
     ap.add_argument("--pmc-mode", action="store_true",
                     help="for rocprofv3 --pmc: launch each variant twice after a cache flush, then a calibration "
                          "kernel that reads and writes 512 MiB, and exit (with --backward: two backward passes per variant)")
@@ -372,6 +405,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.varlen:
         return varlen_report(args)
+    if args.configs:
+        return configs_report(args)
     cases = headline_suite() if args.suite == "headline" else north_star_suite()
     if args.variants:
         keep = set(args.variants.split(","))
