@@ -290,8 +290,9 @@ def varlen_report(args) -> int:
 
 def fp8_report(cases, inputs, works, args) -> int:
     """Per variant: the FP8 forward (attention_fp8, e4m3 q / k / v quantised per
-    tensor from the suite's inputs) against the bf16 forward on the same inputs:
-    HIP-event median per call and algorithmic TFLOP/s (4 D per visible pair)."""
+    tensor from the suite's inputs) against the bf16 forward on the same inputs,
+    then the FP8 forward on e5m2 inputs: HIP-event median per call and
+    algorithmic TFLOP/s (4 D per visible pair)."""
     import torch
 
     from chia_proj_amd import OPS, attention_fp8, core_kwargs, quantize_fp8
@@ -306,15 +307,18 @@ def fp8_report(cases, inputs, works, args) -> int:
         (q8, qd), (k8, kd), (v8, vd) = (quantize_fp8(t) for t in (q, k, v))
         us8 = median_us(lambda: attention_fp8(q8, k8, v8, q_descale=qd, k_descale=kd, v_descale=vd, **kw))
         us16 = median_us(lambda: OPS[c.op](q, k, v, **params))
+        (q5, qd5), (k5, kd5), (v5, vd5) = (quantize_fp8(t, dtype=torch.float8_e5m2) for t in (q, k, v))
+        us5 = median_us(lambda: attention_fp8(q5, k5, v5, q_descale=qd5, k_descale=kd5, v_descale=vd5, **kw))
         flops = works[c.name]["flops_alg"]
         tf8, tf16 = flops / (us8 * 1e-6) / 1e12, flops / (us16 * 1e-6) / 1e12
         rows[c.op] = {"fp8_us": round(us8, 2), "bf16_us": round(us16, 2), "fp8_tflops_alg": round(tf8, 2),
-                      "pct_fp8_peak": round(100 * tf8 / PEAK_FP8_TFLOPS, 2), "speedup": round(us16 / us8, 3)}
+                      "pct_fp8_peak": round(100 * tf8 / PEAK_FP8_TFLOPS, 2), "speedup": round(us16 / us8, 3),
+                      "e5m2_us": round(us5, 2)}
         tot_fp8 += us8
         tot_bf16 += us16
         tot_flops += flops
         log(f"  fp8 {c.op:22s} {us8:8.1f} us ({tf8:7.1f} TF/s, {100 * tf8 / PEAK_FP8_TFLOPS:5.1f}% of fp8 peak)"
-            f"   bf16 {us16:8.1f} us   x{us16 / us8:5.2f}")
+            f"   bf16 {us16:8.1f} us   x{us16 / us8:5.2f}   e5m2 {us5:8.1f} us")
     c0 = cases[0]
     print(json.dumps({
         "metric": "fp8 forward (e4m3 q, k, v) algorithmic TFLOP/s over the ten variants",

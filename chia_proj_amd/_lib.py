@@ -109,6 +109,10 @@ class BwdArgs(ctypes.Structure):
             setattr(self, key, val)
 
 
+FP8_E4M3 = 0  # chia_attn_fp8_args.format: CHIA_ATTN_FP8_E4M3
+FP8_E5M2 = 1  # CHIA_ATTN_FP8_E5M2
+
+
 class Fp8Args(ctypes.Structure):
     """Mirror of ``chia_attn_fp8_args``."""
 

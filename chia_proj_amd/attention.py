@@ -302,18 +302,24 @@ def run_backward(do, q, k, v, o, lse, params):
     return dq, dk, dv
 
 
-# ---- FP8 (e4m3) operands ----------------------------------------------------------
+# ---- FP8 (e4m3 / e5m2) operands ---------------------------------------------------
 
 FP8_DTYPE = torch.float8_e4m3fn
 FP8_MAX = 448.0
+# storage formats of q, k, v: torch dtype -> (chia_attn_fp8_args.format, largest finite value)
+FP8_FORMATS = {torch.float8_e4m3fn: (_lib.FP8_E4M3, 448.0), torch.float8_e5m2: (_lib.FP8_E5M2, 57344.0)}
 
 
-def quantize_fp8(x: torch.Tensor, amax: Optional[float] = None):
-    """Per-tensor e4m3 quantisation: (x8, descale) with x ~= x8.float() * descale;
-    the scale maps max |x| (or `amax`) to 448, the e4m3 maximum."""
+def quantize_fp8(x: torch.Tensor, amax: Optional[float] = None, dtype: torch.dtype = FP8_DTYPE):
+    """Per-tensor FP8 quantisation: (x8, descale) with x ~= x8.float() * descale;
+    the scale maps max |x| (or `amax`) to the format's largest finite value
+    (448 for e4m3, the default; 57344 for torch.float8_e5m2)."""
+    if dtype not in FP8_FORMATS:
+        raise TypeError(f"dtype must be torch.float8_e4m3fn or torch.float8_e5m2, got {dtype}")
+    top = FP8_FORMATS[dtype][1]
     a = float(x.detach().abs().max()) if amax is None else float(amax)
-    descale = a / FP8_MAX if a > 0 and math.isfinite(a) else 1.0
-    x8 = (x.float() / descale).clamp(-FP8_MAX, FP8_MAX).to(FP8_DTYPE)
+    descale = a / top if a > 0 and math.isfinite(a) else 1.0
+    x8 = (x.float() / descale).clamp(-top, top).to(dtype)
     return x8, descale
 
 
@@ -323,14 +329,17 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
                   scale: Optional[float] = None, head_scale: PerHead = None, alibi_slopes: PerHead = None,
                   softcap: float = 0.0, bias: float = 0.0, post_scale: float = 1.0,
                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """attention() on float8 e4m3 q, k, v ([B, H, S, D] / [B, H_kv, S, D]) with
-    per-tensor descales (real = stored * descale); returns bf16 o.  Both products
-    run on the gfx950 FP8 matrix path (chia_attn_fwd_fp8); the attention weights
-    are rounded to e4m3 (after scaling by 2^8).  Forward only."""
+    """attention() on float8 q, k, v ([B, H, S, D] / [B, H_kv, S, D]), all three
+    torch.float8_e4m3fn or all three torch.float8_e5m2, with per-tensor descales
+    (real = stored * descale); returns bf16 o.  Both products run on the gfx950
+    FP8 matrix path (chia_attn_fwd_fp8); the attention weights are rounded to
+    e4m3 (after scaling by 2^8).  Forward only."""
     for name, t in (("q", q), ("k", k), ("v", v)):
-        if not isinstance(t, torch.Tensor) or t.dtype != FP8_DTYPE:
-            raise TypeError(f"{name} must be a torch.float8_e4m3fn tensor, got "
+        if not isinstance(t, torch.Tensor) or t.dtype not in FP8_FORMATS:
+            raise TypeError(f"{name} must be a torch.float8_e4m3fn or torch.float8_e5m2 tensor, got "
                             f"{getattr(t, 'dtype', type(t).__name__)}")
+        if t.dtype != q.dtype:
+            raise TypeError(f"q, k and v must share one FP8 format, got {q.dtype} and {t.dtype}")
         if t.dim() != 4:
             raise ValueError(f"{name} must be 4-D, got shape {tuple(t.shape)}")
     B, H, S, D = q.shape
@@ -369,8 +378,8 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
         st[0], st[1], st[2] = t.stride(0), t.stride(1), t.stride(2)
     a.head_scale = hs.data_ptr() if hs is not None else None
     a.alibi_slopes = sl.data_ptr() if sl is not None else None
-    f = _lib.Fp8Args(attn=ctypes.pointer(a), q_descale=float(q_descale), k_descale=float(k_descale),
-                     v_descale=float(v_descale))
+    f = _lib.Fp8Args(format=FP8_FORMATS[q.dtype][0], attn=ctypes.pointer(a), q_descale=float(q_descale),
+                     k_descale=float(k_descale), v_descale=float(v_descale))
     with torch.cuda.device(q.device):
         _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
     return o

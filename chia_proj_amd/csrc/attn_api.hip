@@ -20,7 +20,7 @@ KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
 KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d128(int norm, bool alibi, bool softcap);
-Fp8KernelFn select_fp8_kernel(int head_dim, int norm, bool alibi, bool softcap);
+Fp8KernelFn select_fp8_kernel(int head_dim, int format, int norm, bool alibi, bool softcap);
 
 namespace {
 
@@ -326,7 +326,7 @@ extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
 
 extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
   if (!fa) return CHIA_ATTN_ERR_NULL;
-  if (fa->struct_size != sizeof(chia_attn_fp8_args) || fa->format != 0) return CHIA_ATTN_ERR_STRUCT;
+  if (fa->struct_size != sizeof(chia_attn_fp8_args) || fa->format > CHIA_ATTN_FP8_E5M2) return CHIA_ATTN_ERR_STRUCT;
   for (int i = 0; i < 5; ++i)
     if (fa->reserved[i] != 0) return CHIA_ATTN_ERR_STRUCT;
   const chia_attn_args* a = fa->attn;
@@ -369,7 +369,8 @@ extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
   p.softcap = a->softcap;
   p.bias = a->bias;
   p.post_scale = a->post_scale;
-  const Fp8KernelFn fn = select_fp8_kernel((int)a->head_dim, (int)a->norm, a->alibi_slopes != nullptr, a->softcap > 0.f);
+  const Fp8KernelFn fn = select_fp8_kernel((int)a->head_dim, (int)fa->format, (int)a->norm, a->alibi_slopes != nullptr,
+                                           a->softcap > 0.f);
   if (!fn) return CHIA_ATTN_ERR_NORM;
   void* kargs[] = {&p};
   hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(256), kargs, 0,

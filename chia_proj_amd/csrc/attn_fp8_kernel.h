@@ -1,7 +1,7 @@
-// attn_fp8_kernel.h -- gfx950 forward attention with FP8 (OCP e4m3) operands.
+// attn_fp8_kernel.h -- gfx950 forward attention with FP8 (OCP e4m3 or e5m2) operands.
 //
 // Semantics: the forward of attn_fwd_kernel.h (mask, score modifiers,
-// normalisers) for q, k, v stored as float8 e4m3 with per-tensor
+// normalisers) for q, k, v stored as float8 e4m3 or e5m2 with per-tensor
 // dequantisation factors (real value = stored value * descale); o is bf16.
 // Both products run on v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales),
 // twice the bf16 matrix rate:
@@ -37,7 +37,8 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2_t lds_i32x2_t;
 
-constexpr int kFp8E4M3 = 0;  // MFMA operand format code (cbsz / blgp)
+constexpr int kFp8E4M3 = 0;  // MFMA operand format codes (cbsz / blgp): OCP e4m3
+constexpr int kFp8E5M2 = 1;  //   and OCP e5m2
 constexpr float kFp8Max = 448.0f;
 // Softmax weights are 2^(x - m + kFp8Pre) with a running max m that moves
 // only when a tile's max exceeds it by more than kFp8Lazy: weights <= 2^8.
@@ -93,8 +94,11 @@ __device__ __forceinline__ int pk_fp8(float a, float b, int old) {
   return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, HI);
 }
 
-template <int D, int NORM, bool ALIBI, bool SOFTCAP>
+// FMT: the storage format of q, k and v (kFp8E4M3 or kFp8E5M2); the weights
+// P are e4m3 in either case.
+template <int D, int NORM, bool ALIBI, bool SOFTCAP, int FMT>
 __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p) {
+  static_assert(FMT == kFp8E4M3 || FMT == kFp8E5M2, "q, k, v are e4m3 or e5m2");
   constexpr int NW = 4, BN = 64, KB = 2;
   constexpr int RP = D;                 // LDS row pitch (bytes)
   constexpr int T_BYTES = BN * RP;
@@ -198,7 +202,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
         const i32x4_t lo = *(const i32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0));
         const i32x4_t hi = *(const i32x4_t*)(St + kr * RP + 16 * fp8_slot<D>(kr, c0 + 1));
         const i32x8_t a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-        sacc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qf[kc], sacc[kb], kFp8E4M3, kFp8E4M3, 0,
+        sacc[kb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, qf[kc], sacc[kb], FMT, FMT, 0,
                                                                   0x7f7f7f7f, 0, 0x7f7f7f7f);
       }
     }
@@ -345,7 +349,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
       const i32x8_t va = __builtin_shufflevector(__builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3),
                                                  __builtin_shufflevector(t2[2], t2[3], 0, 1, 2, 3), 0, 1, 2, 3, 4, 5,
                                                  6, 7);
-      oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, pb, oacc[db], kFp8E4M3, kFp8E4M3, 0, 0x7f7f7f7f,
+      oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, pb, oacc[db], FMT, kFp8E4M3, 0, 0x7f7f7f7f,
                                                                  0, 0x7f7f7f7f);
     }
   }

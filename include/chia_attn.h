@@ -175,16 +175,20 @@ int64_t chia_attn_bwd_workspace_size(const chia_attn_args* fwd);
 int chia_attn_bwd(const chia_attn_bwd_args* args, void* stream);
 
 /* FP8 forward.  `attn` describes the call as for chia_attn_fwd, with q, k, v
- * pointing at float8 e4m3 data (OCP e4m3fn: 4 exponent bits, bias 7, max 448;
- * strides in elements = bytes, multiples of 16; 16-byte aligned) and o at
- * bf16 [B, H, S, D].  Real values are stored values times the descales.  Both
- * products run on the gfx950 FP8 matrix path (twice the bf16 rate): the
- * weights are rounded to e4m3 after scaling by 2^8, the accumulation is fp32;
- * ReLU weights above 448 saturate.  cu_seqlens is not supported (NULL).  No
- * counterpart in the reference, whose kernels are bf16 only. */
+ * pointing at float8 data of one format (`format`: OCP e4m3fn -- 4 exponent
+ * bits, bias 7, max 448 -- or OCP e5m2 -- 5 exponent bits, bias 15, max
+ * 57344; strides in elements = bytes, multiples of 16; 16-byte aligned) and o
+ * at bf16 [B, H, S, D].  Real values are stored values times the descales.
+ * Both products run on the gfx950 FP8 matrix path (twice the bf16 rate): the
+ * weights are rounded to e4m3 after scaling by 2^8 (for either input format),
+ * the accumulation is fp32; ReLU weights above 448 saturate.  cu_seqlens is
+ * not supported (NULL).  No counterpart in the reference, whose kernels are
+ * bf16 only. */
+#define CHIA_ATTN_FP8_E4M3 0u
+#define CHIA_ATTN_FP8_E5M2 1u
 typedef struct chia_attn_fp8_args {
   uint32_t struct_size;        /* sizeof(chia_attn_fp8_args) */
-  uint32_t format;             /* 0 = e4m3 for q, k and v (the only format) */
+  uint32_t format;             /* CHIA_ATTN_FP8_E4M3 or CHIA_ATTN_FP8_E5M2: q, k and v */
   const chia_attn_args* attn;  /* shapes, strides, mask, score, normaliser; q, k, v fp8; o bf16 */
   float q_descale, k_descale, v_descale;  /* > 0, finite */
   int32_t reserved[5];         /* must be zero */

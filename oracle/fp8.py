@@ -2,8 +2,8 @@
 TEST INFRASTRUCTURE ONLY.
 
 The reference has no FP8 path (its kernels are bf16); the FP8 forward's
-semantics are attention() of the DEQUANTISED inputs (stored e4m3 value times
-its per-tensor descale), so `fp8_ref` is generic.attention_ref on those
+semantics are attention() of the DEQUANTISED inputs (stored e4m3 or e5m2 value
+times its per-tensor descale), so `fp8_ref` is generic.attention_ref on those
 values.  `fp8_emulated` adds the one rounding the FP8 path introduces besides
 its inputs: the attention weights are scaled by 2^8 and rounded to e4m3 (torch's
 float8_e4m3fn cast: round to nearest even), the row sum keeps the unrounded

@@ -236,8 +236,8 @@ def test_fp8_rejects_bad_arguments_without_launching(lib_built):
     f = _lib.Fp8Args(attn=ctypes.pointer(a))
     call = lambda: lib_built.chia_attn_fwd_fp8(ctypes.byref(f), None)  # noqa: E731
     assert lib_built.chia_attn_fwd_fp8(None, None) == -1
-    f.format = 1
-    assert call() == -8                      # only e4m3
+    f.format = 2
+    assert call() == -8                      # e4m3 (0) or e5m2 (1) only
     f.format = 0
     f.reserved[4] = 1
     assert call() == -8

@@ -1,7 +1,7 @@
 """GPU parity of the FP8 forward (chia_attn_fwd_fp8 through attention_fp8).
 
-Reference: attention of the dequantised e4m3 inputs (oracle/fp8.py::fp8_ref,
-fp32).  Gate (per (b, h) slice, relative to s = max(1, max |ref|)): the
+Reference: attention of the dequantised e4m3 (or e5m2) inputs
+(oracle/fp8.py::fp8_ref, fp32).  Gate (per (b, h) slice, relative to s = max(1, max |ref|)): the
 kernel's error may exceed twice the error of the FP8 rounding model
 (oracle/fp8.py::fp8_emulated: the weights rounded to e4m3 after scaling by
 2^8) by at most the bf16 gate -- max 2e-2 s, mean 2e-3 s.  FP8 is the gate
@@ -20,11 +20,11 @@ def _say(msg):
     print(msg, flush=True)
 
 
-def _inputs(B, H, Hkv, S, D, seed):
+def _inputs(B, H, Hkv, S, D, seed, dtype=torch.float8_e4m3fn):
     g = torch.Generator("cpu").manual_seed(seed)
     q = torch.randn(B, H, S, D, generator=g)
     k, v = (torch.randn(B, Hkv, S, D, generator=g) for _ in range(2))
-    return [quantize_fp8(t) for t in (q, k, v)]
+    return [quantize_fp8(t, dtype=dtype) for t in (q, k, v)]
 
 
 def _check(name, qkv, kw):
@@ -93,3 +93,21 @@ def test_deterministic_and_close_to_bf16():
     b = attention_fp8(q8.to(DEV), k8.to(DEV), v8.to(DEV), q_descale=qd, k_descale=kd, v_descale=vd, causal=True,
                       window=300)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("op", list(OPS))
+@pytest.mark.parametrize("D", [64, 128])
+def test_e5m2_inputs(op, D):
+    """q, k, v stored as OCP e5m2 (format 1: the matrix path reads them as bf8),
+    weights still e4m3; same gate against the attention of the dequantised values."""
+    _say(f"[fp8] e5m2 {op} D={D}")
+    kw = _variant_kwargs(op, 4)
+    qkv = _inputs(1, 4, 4, 520, D, 3100 + D, dtype=torch.float8_e5m2)
+    assert qkv[0][0].dtype == torch.float8_e5m2
+    _check(f"e5m2 {op} D={D}", qkv, kw)
+
+
+def test_e5m2_gqa_and_edges():
+    _say("[fp8] e5m2 gqa / ragged")
+    _check("e5m2 gqa window", _inputs(2, 4, 2, 333, 64, 77, dtype=torch.float8_e5m2), dict(causal=True, window=100))
+    _check("e5m2 S1", _inputs(1, 2, 2, 1, 128, 78, dtype=torch.float8_e5m2), dict(causal=True))

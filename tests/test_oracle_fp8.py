@@ -47,3 +47,28 @@ def test_quantize_round_trip():
     assert x8.dtype == torch.float8_e4m3fn and abs(d - x.abs().max().item() / 448.0) < 1e-12
     back = x8.float() * d
     assert ((back - x).abs() <= (x.abs() * 2 ** -4) + 2 ** -9 * d).all()
+
+
+def test_e5m2_format_and_round_trip():
+    """torch.float8_e5m2 is OCP e5m2 (bias 15, 2 mantissa bits, max 57344): the
+    storage format 1 of chia_attn_fwd_fp8; quantize_fp8 maps max |x| to 57344."""
+    bits = lambda x: int(torch.tensor([x]).to(torch.float8_e5m2).view(torch.uint8))  # noqa: E731
+    assert bits(1.0) == 0x3C and bits(-2.0) == 0xC0 and bits(57344.0) == 0x7B
+    assert bits(2.0 ** -14) == 0x04 and bits(2.0 ** -16) == 0x01          # smallest normal, smallest subnormal
+    x = torch.randn(1000, generator=torch.Generator().manual_seed(4)) * 3
+    x8, d = quantize_fp8(x, dtype=torch.float8_e5m2)
+    assert x8.dtype == torch.float8_e5m2 and abs(d - x.abs().max().item() / 57344.0) < 1e-12
+    back = x8.float() * d
+    assert ((back - x).abs() <= (x.abs() * 2 ** -3) + 2 ** -17 * d).all()
+    with pytest.raises(TypeError):
+        quantize_fp8(x, dtype=torch.float16)
+
+
+def test_mixed_formats_are_rejected_before_any_launch():
+    from chia_proj_amd import attention_fp8
+    q = torch.zeros(1, 1, 4, 64).to(torch.float8_e4m3fn)
+    k = torch.zeros(1, 1, 4, 64).to(torch.float8_e5m2)
+    with pytest.raises(TypeError):
+        attention_fp8(q, k, k)
+    with pytest.raises(TypeError):
+        attention_fp8(q.float(), q, q)
