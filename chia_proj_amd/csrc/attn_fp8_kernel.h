@@ -20,7 +20,8 @@
 //                             + 8 (t >> 2), columns d0 + 8p, hands lane j + 8p
 //                             the four-key groups of dwords 2 wp, 2 wp + 1 of
 //                             column d0 + 8p + j -- the keys of the B operand.
-// The row sum adds the unrounded fp32 weights.  Softmax weights are
+// The row sum adds the unrounded fp32 weights (D = 128) or, on the matrix
+// core, the e4m3 weights (D = 64 softmax).  Softmax weights are
 // 2^(x - m + 4) with a running max m that moves (rescaling O and l) only when
 // a tile's max exceeds it by more than 4 (log2): weights stay <= 2^8 < 448,
 // the e4m3 maximum, and weights down to 2^-13 of the row max stay normal.
@@ -161,6 +162,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
+  // D = 64 softmax: the row sums come from the matrix core, as one more block
+  // of O^T whose V^T rows are all ones (e4m3 1.0 = 0x38): every register of
+  // lsum holds the sum of the lane's row's e4m3 weights.  One MFMA per tile
+  // replaces 32 VALU adds per lane, and the kernels are VALU-bound.
+  constexpr bool kMfmaSum = NORM == NORM_SOFTMAX && D == 64;
+  f32x16_t lsum;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) lsum[e] = 0.f;
 
   // LDS lane offsets.  K rows (A operand of S^T): row 32 kb + lq, chunks 4 kc + 2 lh (+1).
   // V^T (A operand of O^T) by transposed reads: lane q of 16-lane group G reads key
@@ -285,6 +294,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
       if (__any(m_new != m_run)) {
         const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
+        if constexpr (kMfmaSum)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) lsum[e] *= alpha;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -301,7 +313,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
           else if constexpr (SOFTCAP) arg = __builtin_fmaf(x[kb][e], cA, cB - m_use);
           else arg = x[kb][e] - m_use;
           pw[kb][e] = __builtin_amdgcn_exp2f(arg);
-          l_run += pw[kb][e];
+          if constexpr (!kMfmaSum) l_run += pw[kb][e];
         }
     } else {
       // sigmoid: 2^8 / (1 + 2^(-(t + bias) log2 e)) = rcp(2^-8 e + 2^-8); ReLU: clamp(t, 0, 448)
@@ -352,13 +364,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
       oacc[db] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(va, pb, oacc[db], FMT, kFp8E4M3, 0, 0x7f7f7f7f,
                                                                  0, 0x7f7f7f7f);
     }
+    if constexpr (kMfmaSum) {
+      const i32x8_t ones = {0x38383838, 0x38383838, 0x38383838, 0x38383838,
+                            0x38383838, 0x38383838, 0x38383838, 0x38383838};
+      lsum = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pb, lsum, kFp8E4M3, kFp8E4M3, 0, 0x7f7f7f7f, 0,
+                                                             0x7f7f7f7f);
+    }
   }
 
   // epilogue: o = O^T^T * v_descale / (2^8 l) (softmax) or * v_descale * post / 2^8
   if (ok) {
     float f;
     if constexpr (NORM == NORM_SOFTMAX) {
-      const float lt = xhalf_sum(l_run);
+      const float lt = kMfmaSum ? lsum[0] : xhalf_sum(l_run);
       f = lt > 0.f ? p.v_descale / lt : 0.f;
     } else if constexpr (NORM == NORM_SIGMOID) {
       f = p.v_descale * p.post_scale * (1.0f / 256.0f);
