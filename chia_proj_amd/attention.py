@@ -317,7 +317,10 @@ def quantize_fp8(x: torch.Tensor, amax: Optional[float] = None, dtype: torch.dty
     if dtype not in FP8_FORMATS:
         raise TypeError(f"dtype must be torch.float8_e4m3fn or torch.float8_e5m2, got {dtype}")
     top = FP8_FORMATS[dtype][1]
-    a = float(x.detach().abs().max()) if amax is None else float(amax)
+    if amax is None:
+        a = float(x.detach().abs().max()) if x.numel() else 0.0
+    else:
+        a = float(amax)
     descale = a / top if a > 0 and math.isfinite(a) else 1.0
     x8 = (x.float() / descale).clamp(-top, top).to(dtype)
     return x8, descale
@@ -334,14 +337,7 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
     (real = stored * descale); returns bf16 o.  Both products run on the gfx950
     FP8 matrix path (chia_attn_fwd_fp8); the attention weights are rounded to
     e4m3 (after scaling by 2^8).  Forward only."""
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        if not isinstance(t, torch.Tensor) or t.dtype not in FP8_FORMATS:
-            raise TypeError(f"{name} must be a torch.float8_e4m3fn or torch.float8_e5m2 tensor, got "
-                            f"{getattr(t, 'dtype', type(t).__name__)}")
-        if t.dtype != q.dtype:
-            raise TypeError(f"q, k and v must share one FP8 format, got {q.dtype} and {t.dtype}")
-        if t.dim() != 4:
-            raise ValueError(f"{name} must be 4-D, got shape {tuple(t.shape)}")
+    _check_fp8(q, k, v, 4)
     B, H, S, D = q.shape
     if (k.shape != v.shape or k.shape[0] != B or k.shape[2:] != q.shape[2:] or k.shape[1] < 1
             or H % k.shape[1] != 0):
@@ -382,6 +378,75 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
                      k_descale=float(k_descale), v_descale=float(v_descale))
     with torch.cuda.device(q.device):
         _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
+    return o
+
+
+def _check_fp8(q, k, v, dims: int):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor) or t.dtype not in FP8_FORMATS:
+            raise TypeError(f"{name} must be a torch.float8_e4m3fn or torch.float8_e5m2 tensor, got "
+                            f"{getattr(t, 'dtype', type(t).__name__)}")
+        if t.dtype != q.dtype:
+            raise TypeError(f"q, k and v must share one FP8 format, got {q.dtype} and {t.dtype}")
+        if t.dim() != dims:
+            raise ValueError(f"{name} must be {dims}-D, got shape {tuple(t.shape)}")
+
+
+def attention_fp8_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                         max_seqlen: Optional[int] = None, *, q_descale: float = 1.0, k_descale: float = 1.0,
+                         v_descale: float = 1.0, norm: str = "softmax", causal: bool = True, window: int = 0,
+                         dilation: int = 1, block: int = 0, prefix: int = 0, scale: Optional[float] = None,
+                         head_scale: PerHead = None, alibi_slopes: PerHead = None, softcap: float = 0.0,
+                         bias: float = 0.0, post_scale: float = 1.0,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """attention_fp8() over a packed batch: q [T, H, D], k / v [T, H_kv, D] float8
+    (one format for the three), cu_seqlens [B + 1] token offsets as for
+    attention_varlen(); returns bf16 o [T, H, D].  Forward only."""
+    _check_fp8(q, k, v, 3)
+    T, H, D = q.shape
+    if (k.shape != v.shape or k.shape[0] != T or k.shape[2] != D or k.shape[1] < 1 or H % k.shape[1] != 0):
+        raise ValueError(f"k and v must be [T, H_kv, D] with H_kv dividing q's H, got {tuple(q.shape)}, "
+                         f"{tuple(k.shape)}, {tuple(v.shape)}")
+    if q.device.type != "cuda" or k.device != q.device or v.device != q.device:
+        raise ValueError("q, k, v must be on the same GPU device")
+    for name, d in (("q_descale", q_descale), ("k_descale", k_descale), ("v_descale", v_descale)):
+        if not (float(d) > 0 and math.isfinite(float(d))):
+            raise ValueError(f"{name} must be finite and > 0, got {d}")
+    if T == 0:
+        check_cu_seqlens(cu_seqlens, 0, max_seqlen)
+        return torch.empty(q.shape, dtype=torch.bfloat16, device=q.device) if out is None else out
+    B, S, cu, order = _cu_plan(cu_seqlens, T, max_seqlen, q.device)
+    sc = _check_params(D, norm, window, dilation, block, prefix, scale, softcap)
+
+    def layout_ok(t):
+        return t.stride(-1) == 1 and t.stride(0) % 16 == 0 and t.stride(1) % 16 == 0 and t.data_ptr() % 16 == 0
+
+    q_, k_, v_ = (t if layout_ok(t) else t.contiguous() for t in (q, k, v))
+    if out is None:
+        o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    else:
+        if out.shape != q.shape or out.dtype != torch.bfloat16 or out.device != q.device or not _layout_ok_packed(out):
+            raise ValueError("out must be a bf16 [T, H, D] tensor like q with unit last stride and 16-byte alignment")
+        o = out
+    hs = _per_head_vector(head_scale, H, q.device, "head_scale", positive=True)
+    sl = _per_head_vector(alibi_slopes, H, q.device, "alibi_slopes", positive=False)
+    a = make_args(batch=B, heads=H, seqlen=max(S, 1), head_dim=D, norm=norm, causal=causal, window=window,
+                  dilation=dilation, block=block, prefix=prefix, scale=sc, softcap=softcap, bias=bias,
+                  post_scale=post_scale)
+    a.q, a.k, a.v, a.o = q_.data_ptr(), k_.data_ptr(), v_.data_ptr(), o.data_ptr()
+    a.kv_heads = k_.shape[1] if k_.shape[1] != H else 0
+    for name, t in (("q_stride", q_), ("k_stride", k_), ("v_stride", v_), ("o_stride", o)):
+        st = getattr(a, name)
+        st[0], st[1], st[2] = 0, t.stride(1), t.stride(0)
+    a.head_scale = hs.data_ptr() if hs is not None else None
+    a.alibi_slopes = sl.data_ptr() if sl is not None else None
+    a.cu_seqlens = cu.data_ptr()
+    a.seq_order = order.data_ptr()
+    f = _lib.Fp8Args(format=FP8_FORMATS[q.dtype][0], attn=ctypes.pointer(a), q_descale=float(q_descale),
+                     k_descale=float(k_descale), v_descale=float(v_descale))
+    with torch.cuda.device(q.device):
+        _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
+    del hs, sl, cu, order  # the launch is queued; torch's allocator orders any reuse after it on this stream
     return o
 
 

@@ -332,7 +332,6 @@ extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
   const chia_attn_args* a = fa->attn;
   const int st = validate(a, true);
   if (st != CHIA_ATTN_OK) return st;
-  if (a->cu_seqlens) return CHIA_ATTN_ERR_SHAPE;
   for (float d : {fa->q_descale, fa->k_descale, fa->v_descale})
     if (!(d > 0.f) || !std::isfinite(d)) return CHIA_ATTN_ERR_SCALE;
   // fp8 rows are D bytes: the 16-byte DMA chunks need byte strides that are multiples of 16
@@ -346,10 +345,12 @@ extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
   p.k = (const uint8_t*)a->k;
   p.v = (const uint8_t*)a->v;
   p.o = (uint16_t*)a->o;
-  p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
-  p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
-  p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
-  p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.q_sb = batch_stride(a, a->q_stride); p.q_sh = a->q_stride[1]; p.q_ss = a->q_stride[2];
+  p.k_sb = batch_stride(a, a->k_stride); p.k_sh = a->k_stride[1]; p.k_ss = a->k_stride[2];
+  p.v_sb = batch_stride(a, a->v_stride); p.v_sh = a->v_stride[1]; p.v_ss = a->v_stride[2];
+  p.o_sb = batch_stride(a, a->o_stride); p.o_sh = a->o_stride[1]; p.o_ss = a->o_stride[2];
+  p.cu_seqlens = a->cu_seqlens;
+  p.seq_order = a->cu_seqlens ? a->seq_order : nullptr;
   p.head_scale = a->head_scale;
   p.alibi_slopes = a->alibi_slopes;
   p.mask = spec_of(a);

@@ -63,6 +63,11 @@ struct Fp8Params {
   float qk_scale;   // scale * q_descale * k_descale
   float v_descale;
   float softcap, bias, post_scale;
+  // Packed sequences (null: fixed length): sequence b is tokens cu_seqlens[b]
+  // .. cu_seqlens[b + 1] - 1 (batch strides 0), mask.S the longest length;
+  // seq_order[i] is the sequence of batch slot i (longest first).
+  const int32_t* cu_seqlens;
+  const int32_t* seq_order;
 };
 
 // Swizzled 16-byte slot of chunk c of row r in an fp8 tile of D-byte rows.
@@ -114,21 +119,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, lh = lane >> 5;
 
-  // workgroup -> (b, h, residue, 128-row block), the blocks with the most keys first
-  const int L = xcd_remap(blockIdx.x, p.n_wg);
+  // workgroup -> (b, h, residue, 128-row block), the blocks with the most keys
+  // first; packed sequences go round-robin to the XCDs (no contiguous ranges)
+  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
   const int bhr = udiv(L, p.div_blk);
   const int blk = p.n_blk - 1 - (L - bhr * p.n_blk);
   const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
-  const int b = udiv(bh, p.div_h), h = bh - b * p.H;
-  const MaskGeom g = residue_geom(p.mask, r);
+  const int bs = udiv(bh, p.div_h), h = bh - bs * p.H;
+  const int b = seq_of(p.seq_order, bs);
+  const SeqSpan seq = seq_span(p.cu_seqlens, b, p.mask.S);
+  MaskSpec ms = p.mask;
+  ms.S = seq.len;
+  const MaskGeom g = residue_geom(ms, r);
   const int nblk_r = (g.S + 127) / 128;
   if (blk >= nblk_r) return;  // whole workgroup, before any barrier
   const int dil = p.mask.dil;
   const int hk = udiv(h, p.div_group);
-  const uint8_t* qh = p.q + b * p.q_sb + h * p.q_sh + r * p.q_ss;
-  const uint8_t* kh = p.k + b * p.k_sb + hk * p.k_sh + r * p.k_ss;
-  const uint8_t* vh = p.v + b * p.v_sb + hk * p.v_sh + r * p.v_ss;
-  uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + r * p.o_ss;
+  const int64_t t0 = seq.tok0 + r;  // the residue's first token
+  const uint8_t* qh = p.q + b * p.q_sb + h * p.q_sh + t0 * p.q_ss;
+  const uint8_t* kh = p.k + b * p.k_sb + hk * p.k_sh + t0 * p.k_ss;
+  const uint8_t* vh = p.v + b * p.v_sb + hk * p.v_sh + t0 * p.v_ss;
+  uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + t0 * p.o_ss;
   const int64_t qrs = p.q_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil, ors = p.o_ss * dil;
 
   // per-head score constants: x = log2-domain score (softmax) or the score itself

@@ -181,9 +181,9 @@ int chia_attn_bwd(const chia_attn_bwd_args* args, void* stream);
  * at bf16 [B, H, S, D].  Real values are stored values times the descales.
  * Both products run on the gfx950 FP8 matrix path (twice the bf16 rate): the
  * weights are rounded to e4m3 after scaling by 2^8 (for either input format),
- * the accumulation is fp32; ReLU weights above 448 saturate.  cu_seqlens is
- * not supported (NULL).  No counterpart in the reference, whose kernels are
- * bf16 only. */
+ * the accumulation is fp32; ReLU weights above 448 saturate.  Packed
+ * sequences (cu_seqlens, seq_order) work as for chia_attn_fwd.  No
+ * counterpart in the reference, whose kernels are bf16 only. */
 #define CHIA_ATTN_FP8_E4M3 0u
 #define CHIA_ATTN_FP8_E5M2 1u
 typedef struct chia_attn_fp8_args {

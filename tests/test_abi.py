@@ -250,5 +250,5 @@ def test_fp8_rejects_bad_arguments_without_launching(lib_built):
     a.q_stride[2] = 72                       # a multiple of 8 elements, not of 16 bytes
     assert call() == -7
     a.q_stride[2] = 64
-    a.cu_seqlens = 0x2000                    # packed sequences: not on the fp8 path
-    assert call() == -2
+    a.cu_seqlens = 0x2002                    # packed sequences: offsets must be 4-byte aligned
+    assert call() == -7

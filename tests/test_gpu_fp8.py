@@ -111,3 +111,58 @@ def test_e5m2_gqa_and_edges():
     _say("[fp8] e5m2 gqa / ragged")
     _check("e5m2 gqa window", _inputs(2, 4, 2, 333, 64, 77, dtype=torch.float8_e5m2), dict(causal=True, window=100))
     _check("e5m2 S1", _inputs(1, 2, 2, 1, 128, 78, dtype=torch.float8_e5m2), dict(causal=True))
+
+
+# ---- packed variable-length batches (cu_seqlens) ------------------------------------
+
+def _packed(lens, H, Hkv, D, seed, dtype=torch.float8_e4m3fn):
+    g = torch.Generator("cpu").manual_seed(seed)
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g)
+    k, v = (torch.randn(T, Hkv, D, generator=g) for _ in range(2))
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32)
+    return [quantize_fp8(t, dtype=dtype) for t in (q, k, v)], cu
+
+
+VARLEN = [
+    ("causal_ragged", [130, 1, 0, 257, 64], 4, 4, 64, dict(causal=True)),
+    ("window_gqa_e5m2", [300, 45, 128], 4, 2, 64, dict(causal=True, window=50)),
+    ("dilated_d128", [200, 77, 129], 2, 2, 128, dict(causal=True, dilation=2)),
+    ("sigmoid_local", [96, 250], 2, 1, 64, dict(norm="sigmoid", causal=False, window=40, bias=-2.0)),
+    ("alibi_softcap", [190, 33], 2, 2, 64, dict(causal=True, alibi_slopes=[0.25, 0.5], softcap=10.0)),
+]
+
+
+@pytest.mark.parametrize("name,lens,H,Hkv,D,kw", VARLEN, ids=[c[0] for c in VARLEN])
+def test_varlen_matches_per_sequence_calls(name, lens, H, Hkv, D, kw):
+    """Each packed sequence gives the bits of attention_fp8 on that sequence alone
+    (same kernel, same tiles), and the first one passes the oracle gate."""
+    from chia_proj_amd import attention_fp8_varlen
+    _say(f"[fp8] varlen {name}")
+    dtype = torch.float8_e5m2 if "e5m2" in name else torch.float8_e4m3fn
+    ((q8, qd), (k8, kd), (v8, vd)), cu = _packed(lens, H, Hkv, D, sum(lens) + D, dtype)
+    o = attention_fp8_varlen(q8.to(DEV), k8.to(DEV), v8.to(DEV), cu.to(DEV), q_descale=qd, k_descale=kd,
+                             v_descale=vd, **kw)
+    torch.cuda.synchronize()
+    assert o.shape == q8.shape and o.dtype == torch.bfloat16
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        t0 = int(cu[b])
+        one = lambda t: t[t0:t0 + n].permute(1, 0, 2).unsqueeze(0).contiguous()  # noqa: E731
+        alone = attention_fp8(one(q8).to(DEV), one(k8).to(DEV), one(v8).to(DEV), q_descale=qd, k_descale=kd,
+                              v_descale=vd, **kw)
+        assert torch.equal(o[t0:t0 + n], alone[0].permute(1, 0, 2)), (name, b)
+    n0 = lens[0]
+    one = lambda t: t[:n0].permute(1, 0, 2).unsqueeze(0).contiguous()  # noqa: E731
+    _check(f"varlen {name} seq 0", [(one(q8), qd), (one(k8), kd), (one(v8), vd)], kw)
+
+
+def test_varlen_empty_and_rejections():
+    from chia_proj_amd import attention_fp8_varlen
+    ((q8, qd), (k8, kd), (v8, vd)), cu = _packed([0], 2, 2, 64, 1)
+    o = attention_fp8_varlen(q8.to(DEV), k8.to(DEV), v8.to(DEV), cu.to(DEV))
+    assert o.shape == (0, 2, 64)
+    ((q8, _), (k8, _), (v8, _)), cu = _packed([5, 7], 2, 2, 64, 2)
+    with pytest.raises(ValueError):
+        attention_fp8_varlen(q8.to(DEV), k8.to(DEV), v8.to(DEV), torch.tensor([0, 5, 11], dtype=torch.int32))

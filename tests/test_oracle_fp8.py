@@ -72,3 +72,8 @@ def test_mixed_formats_are_rejected_before_any_launch():
         attention_fp8(q, k, k)
     with pytest.raises(TypeError):
         attention_fp8(q.float(), q, q)
+
+
+def test_quantize_empty_tensor():
+    x8, d = quantize_fp8(torch.empty(0, 2, 64))
+    assert x8.shape == (0, 2, 64) and d == 1.0
