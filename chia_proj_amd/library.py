@@ -199,3 +199,38 @@ def call_fwd_varlen(q: Tensor, k: Tensor, v: Tensor, cu_seqlens: Tensor, max_seq
                                           params["head_scale"], params["alibi_slopes"],
                                           float(params["softcap"] or 0.0), float(params["bias"]),
                                           float(params["post_scale"]))
+
+
+# ---- FP8 forward -----------------------------------------------------------------
+
+@torch.library.custom_op(f"{NAMESPACE}::fwd_fp8", mutates_args=(), device_types="cuda")
+def fwd_fp8(q: Tensor, k: Tensor, v: Tensor, q_descale: float, k_descale: float, v_descale: float, norm: str,
+            causal: bool, window: int, dilation: int, block: int, prefix: int, scale: Optional[float],
+            head_scale: Optional[Tensor], alibi_slopes: Optional[Tensor], softcap: float, bias: float,
+            post_scale: float) -> Tensor:
+    from .attention import attention_fp8
+
+    return attention_fp8(q, k, v, q_descale=q_descale, k_descale=k_descale, v_descale=v_descale,
+                         **_params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes,
+                                   softcap, bias, post_scale))
+
+
+@fwd_fp8.register_fake
+def _fwd_fp8_fake(q, k, v, q_descale, k_descale, v_descale, norm, causal, window, dilation, block, prefix, scale,
+                  head_scale, alibi_slopes, softcap, bias, post_scale):
+    torch._check(q.dim() == 4, lambda: "q must be 4-D [B, H, S, D]")
+    return torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+
+
+def call_fwd_fp8(q: Tensor, k: Tensor, v: Tensor, q_descale: float, k_descale: float, v_descale: float,
+                 params: dict) -> Tensor:
+    """torch.ops.chia_attn.fwd_fp8 with attention_fp8()'s keyword parameters (per-head
+    vectors float32 device tensors or None; scale None = default)."""
+    return torch.ops.chia_attn.fwd_fp8(q, k, v, float(q_descale), float(k_descale), float(v_descale),
+                                       params["norm"], bool(params["causal"]), int(params["window"] or 0),
+                                       int(params["dilation"] or 1), int(params["block"] or 0),
+                                       int(params["prefix"] or 0),
+                                       None if params["scale"] is None else float(params["scale"]),
+                                       params["head_scale"], params["alibi_slopes"],
+                                       float(params["softcap"] or 0.0), float(params["bias"]),
+                                       float(params["post_scale"]))

@@ -77,3 +77,19 @@ def test_torch_compile_fullgraph_on_meta():
     assert q.grad.shape == q.shape and k.grad.shape == k.shape
     with torch.no_grad():
         assert cf(q, k, v).shape == q.shape
+
+
+def test_fp8_forward_fake_and_compile_on_meta():
+    """chia_attn::fwd_fp8: bf16 output of q's shape from float8 inputs of either
+    format, one node under make_fx."""
+    for dt in (torch.float8_e4m3fn, torch.float8_e5m2):
+        q = torch.empty(2, 4, 100, 64, device="meta", dtype=dt)
+        k = torch.empty(2, 2, 100, 64, device="meta", dtype=dt)
+        o = torch.ops.chia_attn.fwd_fp8(q, k, k, 0.5, 0.25, 1.0, "softmax", True, 0, 1, 0, 0, None, None, None,
+                                        0.0, 0.0, 1.0)
+        assert o.shape == q.shape and o.dtype == torch.bfloat16
+    fn = lambda q, k: torch.ops.chia_attn.fwd_fp8(q, k, k, 1.0, 1.0, 1.0, "relu", False, 0, 1, 0, 0, None,  # noqa
+                                                  None, None, 0.0, 0.0, 1.0)
+    g = make_fx(fn, tracing_mode="fake")(q, k)
+    calls = [n for n in g.graph.nodes if n.op == "call_function"]
+    assert [str(n.target) for n in calls] == ["chia_attn.fwd_fp8.default"]
