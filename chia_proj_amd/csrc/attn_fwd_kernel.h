@@ -233,6 +233,12 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   static_assert(RP % 128 == 0, "rows must be whole multiples of 128 bytes for the XOR offsets");
   static_assert(KB == 2, "a WIDE step covers the two key blocks of a tile");
   constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
+  // ALiBi without softcap: the bias enters the QK^T accumulator as its initial
+  // value, (sl / c1)(j - i) (c1 > 0), so the MFMA returns (biased score) / c1
+  // and the normaliser takes its unbiased form -- one VALU per score fewer than
+  // adding the bias afterwards.  Softmax then runs the plain exponent.
+  constexpr bool kBiasInit = ALIBI && !SOFTCAP;
+  constexpr bool kScaledSoftmax = kPlainSoftmax || (kBiasInit && NORM == NORM_SOFTMAX);  // exponent fma(s, kq, -m)
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
   // Softcapped softmax keeps r = 1 / (1 + 2^(2 s log2e / cap)) per score; the
   // capped score in log2 units is t = sc_a r + sc_b (sc_a < 0), folded into
@@ -323,6 +329,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     ks = sl;
   }
   const float post = kRawRelu ? p.post_scale * c1 : p.post_scale;
+  const float bq = kBiasInit ? sl / c1 : 0.f;  // ALiBi bias per key step, in units of q . k
   // Plain sigmoid: Q is pre-scaled by kq (one bf16 rounding per element, at
   // load), so a score is already the exponent, and the bias enters as the
   // factor 2^k0: p = 1 / (1 + 2^k0 2^s).  The host routes a bias whose 2^k0
@@ -515,9 +522,16 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     auto kb_base = [&](int kb) { return (kb < KB ? St : St2) + 32 * (kb % KB) * RP; };
     f32x16_t sacc[NSTR];
 #pragma unroll
-    for (int st = 0; st < NSTR; ++st)
+    for (int st = 0; st < NSTR; ++st) {
+      if constexpr (kBiasInit) {
+        const float b0 = bq * (float)(jt0 + 32 * kb_of(st) + 4 * lh - (row0[qb_of(st)] + lq));
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
+        for (int e = 0; e < 16; ++e) sacc[st][e] = __builtin_fmaf(bq, (float)(8 * (e >> 2) + (e & 3)), b0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
+      }
+    }
 
     // S^T = K Q^T, key block by key block.  For plain softmax the wavefront
     // issues its MFMAs (here and in PV) at raised priority, so that the
@@ -539,7 +553,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
     if constexpr (kPlainSoftmax) __builtin_amdgcn_s_setprio(0);
     // score modifier -> t (in place)
-    if constexpr (!kPlainSoftmax && !kRawRelu && !kSigFold) {
+    if constexpr (!kScaledSoftmax && !kRawRelu && !kSigFold) {
 #pragma unroll
       for (int st = 0; st < NSTR; ++st) {
         const int i = row0[qb_of(st)] + lq;
@@ -550,7 +564,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
           const int rc = 8 * (e >> 2) + (e & 3);  // key offset of register e
           const float qk = sacc[st][e];
           float lin;
-          if constexpr (ALIBI) lin = __builtin_fmaf(qk, kq, __builtin_fmaf(ks, (float)rc, ksb));
+          if constexpr (ALIBI && !kBiasInit) lin = __builtin_fmaf(qk, kq, __builtin_fmaf(ks, (float)rc, ksb));
           else if constexpr (NORM == NORM_SIGMOID && !SOFTCAP) lin = __builtin_fmaf(qk, kq, k0);
           else lin = qk * kq;
           if constexpr (kCapR) {
@@ -613,7 +627,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       for (int qb = 0; qb < QB; ++qb) {
         if (WIDE && qb == 0) continue;
         float mx = xhalf_max(mq[qb]);
-        if constexpr (kPlainSoftmax) mx = mx * kq;  // kq > 0
+        if constexpr (kScaledSoftmax) mx = mx * kq;  // kq > 0
         m_new[qb] = (mx > m_run[qb] + kRescaleLog2) ? mx : m_run[qb];
         moved |= m_new[qb] != m_run[qb];
       }
@@ -638,7 +652,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 #pragma unroll
         for (int w = 0; w < 8; ++w) {
           float p0, p1;
-          if constexpr (kPlainSoftmax) {
+          if constexpr (kScaledSoftmax) {
             p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, -m_use));
             p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, -m_use));
           } else if constexpr (kCapR) {

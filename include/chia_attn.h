@@ -96,7 +96,7 @@ typedef struct chia_attn_args {
   float softcap;              /* 0 = off (extra_bench.py:60) */
   float bias;                 /* SIGMOID: added before the sigmoid */
   float post_scale;           /* SIGMOID/RELU: multiplies p */
-  const float* head_scale;    /* device float[heads] or NULL (extra_bench.py:35,54) */
+  const float* head_scale;    /* device float[heads], each > 0, or NULL (extra_bench.py:35,54) */
   const float* alibi_slopes;  /* device float[heads] or NULL (extra_bench.py:36,47-50) */
 
   /* Grouped-query / multi-query attention: K and V have kv_heads heads and
