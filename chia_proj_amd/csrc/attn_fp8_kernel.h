@@ -145,6 +145,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   // per-head score constants: x = log2-domain score (softmax) or the score itself
   const float c1 = p.qk_scale * (p.head_scale ? p.head_scale[h] : 1.0f);
   const float sl = (ALIBI && p.alibi_slopes) ? p.alibi_slopes[h] * (float)dil : 0.0f;
+  // ALiBi without softcap seeds the QK^T accumulator with (sl / c1)(j - i): the
+  // MFMA returns the biased score over c1 and the normalisers take their plain form.
+  constexpr bool kBiasInit = ALIBI && !SOFTCAP;
+  const float bq = kBiasInit ? sl / c1 : 0.0f;
 
   // this wavefront's 32 rows: Q as the MFMA B operand (lane = row, 32 bytes of d per 64)
   const int row0 = blk * 128 + 32 * wave;
@@ -213,8 +217,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     f32x16_t sacc[KB];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
+      if constexpr (kBiasInit) {
+        const float b0 = bq * (float)(jt0 + 32 * kb + 4 * lh - i);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
+        for (int e = 0; e < 16; ++e) sacc[kb][e] = __builtin_fmaf(bq, (float)(8 * (e >> 2) + (e & 3)), b0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
+      }
       const int kr = 32 * kb + lq;
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) {
@@ -228,8 +238,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     }
 
     // scores -> weights (lane = query i; register e of block kb = key jt0 + 32 kb + 8 (e >> 2) + (e & 3) + 4 lh).
-    // Without ALiBi / softcap the score's scale folds into the weight's first operation.
-    constexpr bool kPlain = !ALIBI && !SOFTCAP;
+    // Without softcap (ALiBi is in the accumulator) the score's scale folds into
+    // the weight's first operation.
+    constexpr bool kPlain = !SOFTCAP;
     // x: the score in log2 units for softmax (osc = log2 e), in natural units otherwise.
     //   no softcap: x = osc (c1 s + sl (j - i)) = fma(s, c1 osc, fma(sl osc, rc, base_kb))
     //   softcap:    x = osc cap tanh(u / cap) = fma(r, -2 cap osc, cap osc), r = 1 / (1 + 2^(2 u log2e / cap))
