@@ -85,6 +85,7 @@ struct BwdParams {
 template <int NORM, bool ALIBI, bool SOFTCAP>
 struct ScoreGrad {
   float c1, c1l2, sl, cap, k2cap, post, nbias_l2;
+  float bq;  // sl / c1: the ALiBi bias per key step in units of q . k (accumulator seed)
 
   __device__ __forceinline__ void operator()(float s, float dp, float jmi, float lse2, float delta, float& p,
                                              float& ds) const {
@@ -132,6 +133,7 @@ struct ScoreGrad {
     c1 = c1_;
     c1l2 = c1_ * kLog2e;
     sl = sl_;
+    bq = sl_ / c1_;
   }
 };
 
@@ -255,7 +257,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   uint16_t* dqh = p.dq + b * p.dq_sb + h * p.dq_sh + t0 * p.dq_ss;
   const int64_t qrs = p.q_ss * dil, dors = p.do_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil,
                 dqrs = p.dq_ss * dil;
-  ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
+  // ALiBi without softcap seeds the S accumulator with the bias over c1 and
+  // scores it with the plain (unbiased) formulas.
+  constexpr bool kSeed = ALIBI && !SOFTCAP;
+  ScoreGrad<NORM, ALIBI && !kSeed, SOFTCAP> sg = score_consts<NORM, ALIBI && !kSeed, SOFTCAP>(p);
   sg.set_head(p.scale * (p.head_scale ? p.head_scale[h] : 1.0f),
               (ALIBI && p.alibi_slopes) ? p.alibi_slopes[h] * (float)dil : 0.0f);
 
@@ -327,6 +332,11 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
       f32x16_t sacc, pacc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.f;
+      if constexpr (kSeed) {  // register e: key jt0 + 32 kb + 4 lh + rc(e), query i
+        const float b0 = sg.bq * (float)(jt0 + 32 * kb + 4 * lh - i);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[e] = __builtin_fmaf(sg.bq, (float)(8 * (e >> 2) + (e & 3)), b0);
+      }
 #pragma unroll
       for (int kk = 0; kk < DK; ++kk) {
         const bf16x8_t a = *(const bf16x8_t*)(St + 32 * kb * RP + (k_lane ^ (32 * kk)));
@@ -519,7 +529,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     int cls = wvalid ? classify_tile(g, i0, imin32(i0 + BM - 1, g.S - 1), kc, kd) : (int)TILE_EMPTY;
     if (cls == TILE_EMPTY) continue;
     if (i0 + BM > g.S) cls = TILE_PARTIAL;
-    ScoreGrad<NORM, ALIBI, SOFTCAP> sg = score_consts<NORM, ALIBI, SOFTCAP>(p);
+    constexpr bool kSeed = ALIBI && !SOFTCAP;  // as in the dQ kernel
+    ScoreGrad<NORM, ALIBI && !kSeed, SOFTCAP> sg = score_consts<NORM, ALIBI && !kSeed, SOFTCAP>(p);
     sg.set_head(head_c[hq - hkv * p.G], head_c[kMaxGroup + hq - hkv * p.G]);
     const float* st_stats = (const float*)(St + 2 * T_BYTES);  // [64] lse log2 e, then [64] delta
 
@@ -528,6 +539,11 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
       f32x16_t sacc, pacc;
 #pragma unroll
       for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.f;
+      if constexpr (kSeed) {  // register e: query i0 + 32 qb + 4 lh + rc(e), key j
+        const float b0 = sg.bq * (float)(j - (i0 + 32 * qb + 4 * lh));
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sacc[e] = __builtin_fmaf(-sg.bq, (float)(8 * (e >> 2) + (e & 3)), b0);
+      }
 #pragma unroll
       for (int kk = 0; kk < DK; ++kk) {
         const bf16x8_t a = *(const bf16x8_t*)(St + 32 * qb * RP + (k_lane ^ (32 * kk)));
