@@ -86,6 +86,8 @@ template <int NORM, bool ALIBI, bool SOFTCAP>
 struct ScoreGrad {
   float c1, c1l2, sl, cap, k2cap, post, nbias_l2;
   float bq;  // sl / c1: the ALiBi bias per key step in units of q . k (accumulator seed)
+  float c1k2;   // c1 * k2cap
+  float capl2;  // cap * log2 e
 
   __device__ __forceinline__ void operator()(float s, float dp, float jmi, float lse2, float delta, float& p,
                                              float& ds) const {
@@ -104,21 +106,25 @@ struct ScoreGrad {
         ds = t > 0.0f ? dp * post : 0.0f;
       }
     } else {
-      float u = s * c1;
-      if constexpr (ALIBI) u = __builtin_fmaf(sl, jmi, u);
-      float t = u, dtdu = 1.0f;
+      // u = s c1 (+ sl (j - i)); with softcap t = cap th, th = tanh(u / cap)
+      // = 1 - 2 / (1 + 2^(2 u log2e / cap)), and the cap folds into the
+      // exponent's fma
+      float t, th = 0.0f, dtdu = 1.0f;
       if constexpr (SOFTCAP) {
-        // tanh(u / cap) = 1 - 2 / (1 + 2^(2 u log2e / cap))
-        const float th = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u * k2cap));
-        t = cap * th;
+        const float uk = ALIBI ? __builtin_fmaf(sl, jmi, s * c1) * k2cap : s * c1k2;
+        th = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(uk)), 1.0f);
         dtdu = __builtin_fmaf(-th, th, 1.0f);
+        t = cap * th;
+      } else {
+        t = ALIBI ? __builtin_fmaf(sl, jmi, s * c1) : s * c1;
       }
       float dt;
       if constexpr (NORM == NORM_SOFTMAX) {
-        p = __builtin_amdgcn_exp2f(__builtin_fmaf(t, kLog2e, -lse2));
+        p = __builtin_amdgcn_exp2f(SOFTCAP ? __builtin_fmaf(th, capl2, -lse2) : __builtin_fmaf(t, kLog2e, -lse2));
         dt = p * __builtin_fmaf(dp, c1, -delta);
       } else if constexpr (NORM == NORM_SIGMOID) {
-        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(-t, kLog2e, nbias_l2)));
+        const float z = SOFTCAP ? __builtin_fmaf(-th, capl2, nbias_l2) : __builtin_fmaf(-t, kLog2e, nbias_l2);
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
         p = post * sg;
         dt = dp * p * (1.0f - sg);
       } else {
@@ -134,6 +140,7 @@ struct ScoreGrad {
     c1l2 = c1_ * kLog2e;
     sl = sl_;
     bq = sl_ / c1_;
+    c1k2 = c1_ * k2cap;
   }
 };
 
@@ -155,6 +162,7 @@ __device__ __forceinline__ ScoreGrad<NORM, ALIBI, SOFTCAP> score_consts(const Bw
   ScoreGrad<NORM, ALIBI, SOFTCAP> f;
   f.cap = p.softcap;
   f.k2cap = SOFTCAP ? 2.0f * kLog2e / p.softcap : 0.0f;
+  f.capl2 = p.softcap * kLog2e;
   f.post = p.post_scale;
   f.nbias_l2 = -p.bias * kLog2e;
   f.set_head(p.scale, 0.0f);
