@@ -11,8 +11,13 @@ reference's benchmark does.  Prints ONE JSON line on stdout:
                fraction of the bf16 MFMA peak and of the HBM roofline
   roofline     the dominant (slowest) variant's kernel, its average launch
                duration from HIP events around back-to-back loops of it
+  northstar    the ten variants at the north-star shape B4 H16 S4096 D64: hot and
+               cold us/call, % of bf16 MFMA peak (algorithmic and visited-tile
+               FLOPs), % of the HBM roofline (8 TB/s and the measured copy rate),
+               and which variants meet the >= 50 % visited-tile target
   cpu_baseline the reference's eager path (restated in oracle/) on the host CPU,
-               on a bounded sample, with the GPU output checked on that sample
+               on a bounded sample, with the GPU output checked on that sample;
+               c1_fp32: BASELINE.json configs[0] (fp32 eager softcap) in full
 Everything else goes to stderr.
 """
 from __future__ import annotations
@@ -113,6 +118,197 @@ def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16, reps: int = 5):
         "step_s_scaled": total_s,
         "gate_on_sample": checks,
     }
+
+
+def measure_cases(cases, calls, works, flusher, copy_gbps=None, tag=""):
+    """Per variant: HIP-event median of 3 back-to-back loops (the reference's timer,
+    extra_bench.py:8-22), the cold-cache median of single calls after a cache-evicting
+    write (when `flusher` is given), TFLOP/s (algorithmic, visited-tile, dense), and
+    the fractions of the bf16 MFMA peak and of the HBM roofline -- the 8 TB/s
+    specification, and the box's measured copy rate when `copy_gbps` is given."""
+    from chia_proj_amd.accounting import PEAK_HBM_GBPS, rates
+    from chia_proj_amd.timing import cold_us, median_us
+
+    rows, launch_us = {}, {}
+    for c in cases:
+        w = works[c.name]
+        us = median_us(calls[c.name])
+        r = rates(w, us)
+        launch_us[c.name] = us
+        row = {
+            "us": round(us, 2),
+            "tflops_alg": round(r["tflops_alg"], 2),
+            "tflops_visited": round(r["tflops_visited"], 2),
+            "tflops_dense": round(r["tflops_dense"], 2),
+            "pct_mfma_peak_alg": round(100 * r["frac_mfma_alg"], 2),
+            "pct_mfma_peak_visited": round(100 * r["frac_mfma_visited"], 2),
+            "pct_hbm_roofline": round(100 * r["frac_hbm"], 2),
+            "pct_roofline": round(100 * r["frac_roofline"], 2),
+            "bound": w["bound"],
+            "visible_pct": round(100 * w["visible_frac"], 2),
+            "tile_wave": w["tile_wave"],
+        }
+        if copy_gbps:
+            row["pct_hbm_copy"] = round(100 * r["gbps"] / copy_gbps, 2)
+        if flusher is not None:
+            cu = cold_us(calls[c.name], reps=15, flusher=flusher)
+            rc = rates(w, cu)
+            row["cold_us"] = round(cu, 2)
+            row["cold_tflops_alg"] = round(rc["tflops_alg"], 2)
+            row["cold_pct_mfma_peak_visited"] = round(100 * rc["frac_mfma_visited"], 2)
+            row["cold_pct_hbm_roofline"] = round(100 * rc["frac_hbm"], 2)
+            if copy_gbps:
+                row["cold_pct_hbm_copy"] = round(100 * rc["gbps"] / copy_gbps, 2)
+        rows[c.op] = row
+        log(f"  {tag}{c.op:22s} {us:9.1f} us  alg {r['tflops_alg']:7.1f} TF/s ({100*r['frac_mfma_alg']:5.1f}% peak)  "
+            f"visited {r['tflops_visited']:7.1f} ({100*r['frac_mfma_visited']:5.1f}%)  "
+            f"HBM {100*r['frac_hbm']:5.1f}%  " + (f"cold {row['cold_us']:.1f} us" if "cold_us" in row else ""))
+    return rows, launch_us
+
+
+def prepare_cases(cases, dev):
+    """Inputs, calls and work figures for a suite; one q, k, v draw per shape serves
+    every variant (extra_bench.py:79-81), each variant keeping its own parameters.
+    Also returns per-variant calls on each variant's own draw (cold inputs)."""
+    from chia_proj_amd import OPS
+    from chia_proj_amd.accounting import work
+    from chia_proj_amd.workloads import draw_inputs
+
+    inputs, calls, works, shared, distinct = {}, {}, {}, {}, {}
+    for c in cases:
+        q, k, v, params = draw_inputs(c, dev)
+        distinct[c.name] = (lambda fn=OPS[c.op], q=q, k=k, v=v, p=params: fn(q, k, v, **p))
+        q, k, v = shared.setdefault(tuple(q.shape), (q, k, v))
+        inputs[c.name] = (q, k, v, params)
+        calls[c.name] = (lambda fn=OPS[c.op], q=q, k=k, v=v, p=params: fn(q, k, v, **p))
+        works[c.name] = work(c.op, c.B, c.H, c.S, c.D, params)
+    return inputs, calls, works, distinct
+
+
+NORTH_STAR_TARGET_PCT = 50.0  # BASELINE.json north_star: >= 50 % of bf16 MFMA peak, visited-tile FLOPs
+
+
+def northstar_report(dev, copy_gbps, cold: bool):
+    """The north-star shape (B4 H16 S4096 D64, all ten variants, BASELINE parameters):
+    hot and cold-cache us/call, % of the bf16 MFMA peak on algorithmic and visited-tile
+    FLOPs, % of the HBM roofline (specification and measured copy), and which variants
+    reach the north star's >= 50 % of MFMA peak on visited-tile FLOPs."""
+    import torch
+
+    from chia_proj_amd.timing import CacheFlusher
+    from chia_proj_amd.workloads import north_star_suite
+
+    cases = north_star_suite()
+    log("[bench] north-star shape B4 H16 S4096 D64")
+    inputs, calls, works, distinct = prepare_cases(cases, dev)
+    del distinct
+    flusher = CacheFlusher(device=dev) if cold else None
+    rows, launch_us = measure_cases(cases, calls, works, flusher, copy_gbps, tag="ns ")
+    del flusher, inputs, calls
+    torch.cuda.empty_cache()
+    met = [op for op, r in rows.items() if r["pct_mfma_peak_visited"] >= NORTH_STAR_TARGET_PCT]
+    step_us = sum(launch_us.values())
+    total = sum(w["flops_alg"] for w in works.values())
+    return {
+        "config": {"workload": "ten attention variants, B4 H16 S4096 D64 bf16, BASELINE.json parameters",
+                   "batch": 4, "heads": 16, "seq_len": 4096, "head_dim": 64},
+        "target": f">= {NORTH_STAR_TARGET_PCT:.0f}% of bf16 MFMA peak on visited-tile FLOPs (BASELINE.json north_star)",
+        "variants": rows,
+        "met_target": met,
+        "sum_us": round(step_us, 2),
+        "tflops_alg_over_sum": round(total / (step_us * 1e-6) / 1e12, 2),
+    }
+
+
+# The reference's published A100-SXM4-40GB latencies at its own shape (B2 H32 S2048 D128,
+# reference constants): results/FINAL_flexattention.csv:2-11 (GraphSynth kernels and
+# flex_attention).  Context for the reference-shape suite only, not a target.
+A100_PUBLISHED_US = {
+    "sigmoid_attn": (1073.2, None), "relu_attn": (472.8, None), "temp_perhead": (1863.6, 613.7),
+    "bias_alibi": (841.4, 640.7), "bias_dilated": (1816.7, 570.6), "bias_local": (661.6, 402.1),
+    "bias_block_diagonal": (289.4, 261.0), "bias_prefix_lm": (1389.7, 556.7), "softcap_gemma2": (901.0, 846.8),
+    "bias_sliding_window": (433.0, 226.5),
+}
+
+
+def reference_report(dev, args) -> int:
+    """All ten variants at the reference's benchmark shape and constants (B2 H32 S2048
+    D128, extra_bench.py:5,32-62), called through the glob-compatible <op>_BEST.py
+    modules loaded as extra_bench.py:24-27 loads them; HIP-event median and cold-cache
+    us/call beside the reference's published A100 latencies (context, not a target)."""
+    import glob
+    import importlib.util
+
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, rates
+    from chia_proj_amd.timing import CacheFlusher, cold_us, median_us
+    from chia_proj_amd.workloads import draw_inputs, reference_suite
+
+    loaded = {}
+    for path in glob.glob(str(REPO / "chia_proj_amd" / "kernels_mi355x" / "*_BEST.py")):
+        bn = os.path.basename(path).replace("_BEST.py", "")
+        op = "sigmoid_attn" if bn.startswith("sigmoid_") else bn.split("_gemini")[0]
+        spec = importlib.util.spec_from_file_location("k" + str(abs(hash(path))), path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        loaded[op] = mod.launch_kernel
+    from chia_proj_amd.accounting import work
+
+    cases = reference_suite()
+    q, k, v, _ = draw_inputs(cases[0], dev)
+    flusher = CacheFlusher(device=dev)
+    rows, tot_us, tot_flops = {}, 0.0, 0.0
+    for c in cases:
+        fn = lambda f=loaded[c.op]: f(q, k, v)  # noqa: E731
+        w = work(c.op, c.B, c.H, c.S, c.D, {})
+        us = median_us(fn)
+        cu = cold_us(fn, reps=15, flusher=flusher)
+        r = rates(w, us)
+        gs, flex = A100_PUBLISHED_US[c.op]
+        rows[c.op] = {"us": round(us, 2), "cold_us": round(cu, 2), "tflops_alg": round(r["tflops_alg"], 2),
+                      "pct_mfma_peak_alg": round(100 * r["frac_mfma_alg"], 2),
+                      "a100_graphsynth_us": gs, "a100_flex_attention_us": flex}
+        tot_us += us
+        tot_flops += w["flops_alg"]
+        log(f"  ref {c.op:22s} {us:9.1f} us (cold {cu:8.1f})  alg {r['tflops_alg']:7.1f} TF/s "
+            f"({100 * r['frac_mfma_alg']:5.1f}% peak)   A100 GraphSynth {gs} us")
+    print(json.dumps({
+        "metric": "reference benchmark shape: us/call + algorithmic TFLOP/s per variant", "unit": "us",
+        "higher_is_better": False, "dtype": "bf16", "data": "synthetic (seeded N(0,1), one draw for the ten)",
+        "n_gpus": 1,
+        "config": {"workload": "ten variants through <op>_BEST.py::launch_kernel(q, k, v), reference constants, "
+                               "B2 H32 S2048 D128 bf16", "suite": "reference"},
+        "sum_us": round(tot_us, 2), "tflops_alg_over_sum": round(tot_flops / (tot_us * 1e-6) / 1e12, 2),
+        "peak_bf16_tflops": PEAK_BF16_TFLOPS,
+        "a100_context": "results/FINAL_flexattention.csv:2-11 of the reference (A100-SXM4-40GB): context, not a target",
+        "variants": rows,
+    }), flush=True)
+    return 0
+
+
+def cpu_baseline_c1(reps: int = 5):
+    """BASELINE.json configs[0] on the host: the reference's eager path in fp32 (Gemma-2
+    softcap 50, causal, B1 H8 S512 D64; extra_bench.py:37-46,60 with every step in fp32),
+    restated in oracle.variant_ref; median of `reps` after one warm-up."""
+    import torch
+
+    import oracle  # the timed CPU path of this leg only
+    from chia_proj_amd.accounting import work
+    from chia_proj_amd.workloads import baseline_configs, draw_inputs
+
+    case = next(c for c in baseline_configs() if c.name.startswith("c1_"))
+    q, k, v, params = draw_inputs(case, None, dtype=torch.float32)
+    oracle.variant_ref(case.op, q, k, v, heads_per_chunk=case.H, **params)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter_ns()
+        oracle.variant_ref(case.op, q, k, v, heads_per_chunk=case.H, **params)
+        ts.append((time.perf_counter_ns() - t0) * 1e-9)
+    t = statistics.median(ts)
+    flops = work(case.op, case.B, case.H, case.S, case.D, params)["flops_alg"]
+    log(f"  cpu c1 fp32 softcap 50 B1 H8 S512 D64: {t * 1e6:9.1f} us  {flops / t / 1e9:7.2f} GFLOP/s")
+    return {"config": case.name, "dtype": "fp32", "us": round(t * 1e6, 2),
+            "tflops_alg": round(flops / t / 1e12, 5), "cores": torch.get_num_threads(),
+            "sample": f"the whole configuration (B1 H8 S512 D64), median of {reps} after 1 warm-up"}
 
 
 def backward_report(cases, inputs, works, args) -> int:
@@ -367,7 +563,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", default="headline", choices=["headline", "northstar"])
+    ap.add_argument("--suite", default="headline", choices=["headline", "northstar", "reference"],
+                    help="headline: the metric's shape (default); northstar: B4 H16 S4096 D64; reference: the "
+                         "reference's own shape and constants through its loader (own JSON line)")
+    ap.add_argument("--no-northstar", action="store_true",
+                    help="skip the north-star object (B4 H16 S4096 D64) of the default headline run")
     ap.add_argument("--variants", default="", help="comma-separated subset of variants (profiling runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
@@ -399,10 +599,9 @@ def main() -> int:
 
     import torch
 
-    from chia_proj_amd import OPS
-    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, PEAK_HBM_GBPS, rates, work
-    from chia_proj_amd.timing import CacheFlusher, cold_us, copy_calibration, median_us
-    from chia_proj_amd.workloads import draw_inputs, headline_suite, north_star_suite
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, PEAK_HBM_GBPS
+    from chia_proj_amd.timing import CacheFlusher, copy_calibration
+    from chia_proj_amd.workloads import headline_suite, north_star_suite
 
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
@@ -413,6 +612,8 @@ def main() -> int:
         return varlen_report(args)
     if args.configs:
         return configs_report(args)
+    if args.suite == "reference":
+        return reference_report(dev, args)
     cases = headline_suite() if args.suite == "headline" else north_star_suite()
     if args.variants:
         keep = set(args.variants.split(","))
@@ -421,17 +622,7 @@ def main() -> int:
             raise SystemExit(f"no variant matches {args.variants}")
 
     log(f"[bench] device {torch.cuda.get_device_name(0)}  suite={args.suite}  variants={len(cases)}")
-    # One q, k, v per shape serves every variant, as in the reference's benchmark
-    # (extra_bench.py:79-81); each variant keeps its own parameters.  The
-    # per-variant draws stay for the distinct-inputs step below.
-    inputs, calls, works, shared, distinct = {}, {}, {}, {}, {}
-    for c in cases:
-        q, k, v, params = draw_inputs(c, dev)
-        distinct[c.name] = (lambda fn=OPS[c.op], q=q, k=k, v=v, p=params: fn(q, k, v, **p))
-        q, k, v = shared.setdefault(tuple(q.shape), (q, k, v))
-        inputs[c.name] = (q, k, v, params)
-        calls[c.name] = (lambda fn=OPS[c.op], q=q, k=k, v=v, p=params: fn(q, k, v, **p))
-        works[c.name] = work(c.op, c.B, c.H, c.S, c.D, params)
+    inputs, calls, works, distinct = prepare_cases(cases, dev)
     if args.backward:
         return backward_report(cases, inputs, works, args)
     if args.flex:
@@ -455,37 +646,20 @@ def main() -> int:
         print(json.dumps({"pmc_mode": True, "variants": [c.op for c in cases], "calibration_bytes": 2 * x.numel() * 4}))
         return 0
 
+    # The box's achievable HBM rate (a copy larger than the Infinity Cache), so the
+    # HBM fractions can be stated against it as well as against the 8 TB/s spec.
+    calib = None if args.no_calibration else copy_calibration(device=dev)
+    if calib:
+        log(f"[bench] copy calibration: {calib['GBps']:.0f} GB/s = {100*calib['frac_of_peak']:.1f}% of 8 TB/s")
+        if calib["frac_of_peak"] >= 1.0:
+            log("[bench] WARNING: copy exceeded 100% of peak: timer not trustworthy")
+    copy_gbps = calib["GBps"] if calib else None
+
     # ---- per-variant: median of 3 event loops (reference timer), cold cache ----
     # Each loop runs one variant back to back between two events, so the
     # per-launch average is the kernel's own duration (rocprofv3 agrees).
     flusher = None if args.no_cold else CacheFlusher(device=dev)
-    variants = {}
-    launch_us = {}
-    for c in cases:
-        us = median_us(calls[c.name])
-        r = rates(works[c.name], us)
-        launch_us[c.name] = us
-        row = {
-            "us": round(us, 2),
-            "tflops_alg": round(r["tflops_alg"], 2),
-            "tflops_visited": round(r["tflops_visited"], 2),
-            "tflops_dense": round(r["tflops_dense"], 2),
-            "pct_mfma_peak_alg": round(100 * r["frac_mfma_alg"], 2),
-            "pct_mfma_peak_visited": round(100 * r["frac_mfma_visited"], 2),
-            "pct_hbm_roofline": round(100 * r["frac_hbm"], 2),
-            "pct_roofline": round(100 * r["frac_roofline"], 2),
-            "bound": works[c.name]["bound"],
-            "visible_pct": round(100 * works[c.name]["visible_frac"], 2),
-            "tile_wave": works[c.name]["tile_wave"],
-        }
-        if flusher is not None:
-            cu = cold_us(calls[c.name], reps=15, flusher=flusher)
-            row["cold_us"] = round(cu, 2)
-            row["cold_tflops_alg"] = round(works[c.name]["flops_alg"] / (cu * 1e-6) / 1e12, 2)
-        variants[c.op] = row
-        log(f"  {c.op:22s} {us:9.1f} us  alg {r['tflops_alg']:7.1f} TF/s ({100*r['frac_mfma_alg']:5.1f}% peak)  "
-            f"visited {r['tflops_visited']:7.1f}  roofline {100*r['frac_roofline']:5.1f}%  "
-            + (f"cold {row['cold_us']:.1f} us" if "cold_us" in row else ""))
+    variants, launch_us = measure_cases(cases, calls, works, flusher, copy_gbps)
     del flusher
 
     # ---- timed steps: W warm-up, then K steps bracketed by synchronize ----------
@@ -525,7 +699,6 @@ def main() -> int:
     del distinct
     log(f"[bench] distinct inputs per variant: {step_distinct_ms:.3f} ms/step")
 
-
     # ---- dominant kernel roofline (HIP events around its back-to-back loops) ----
     dom = max(cases, key=lambda c: launch_us[c.name])
     w = works[dom.name]
@@ -542,16 +715,15 @@ def main() -> int:
         "algorithmic_per_launch": per_launch,
     }
 
-    calib = None if args.no_calibration else copy_calibration(device=dev)
-    if calib:
-        log(f"[bench] copy calibration: {calib['GBps']:.0f} GB/s = {100*calib['frac_of_peak']:.1f}% of 8 TB/s")
-        if calib["frac_of_peak"] >= 1.0:
-            log("[bench] WARNING: copy exceeded 100% of peak: timer not trustworthy")
+    northstar = None
+    if args.suite == "headline" and not args.no_northstar and not args.variants:
+        northstar = northstar_report(dev, copy_gbps, cold=not args.no_cold)
 
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline (reference eager path on the host)")
         cpu = cpu_baseline(cases, inputs, outputs)
+        cpu["c1_fp32"] = cpu_baseline_c1()
 
     total_flops = sum(works[c.name]["flops_alg"] for c in cases)
     c0 = cases[0]
@@ -580,6 +752,7 @@ def main() -> int:
                                  "value": round(total_flops / (step_distinct_ms * 1e-3) / 1e12, 2),
                                  "note": "each variant on its own q, k, v draw: every launch reads cold inputs"},
         "variants": variants,
+        "northstar": northstar,
         "copy_calibration": calib,
         "peak": {"bf16_mfma_tflops": PEAK_BF16_TFLOPS, "hbm_gbps": PEAK_HBM_GBPS},
     }

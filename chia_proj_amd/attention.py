@@ -281,7 +281,10 @@ def _op_forward(q, k, v, params):
 
 def run_backward(do, q, k, v, o, lse, params):
     """dq, dk, dv by chia_attn_bwd (lse: the forward's float32 [B, H, S], softmax only)."""
-    a, _, _, (q_, k_, v_), _ = _prepare(q, k, v, o, **params)
+    # q_, k_, v_ (layout copies where needed) and the per-head vectors hs, sl stay
+    # referenced until the launch is queued: do_, dq, dk, dv and the workspace are
+    # allocated below and must not take their memory.
+    a, hs, sl, (q_, k_, v_), _ = _prepare(q, k, v, o, **params)
     do_ = do if (do.dtype == torch.bfloat16 and _layout_ok(do)) else do.to(torch.bfloat16).contiguous()
     if do_.shape != q.shape:
         raise ValueError(f"do must have q's shape {tuple(q.shape)}, got {tuple(do.shape)}")
@@ -299,6 +302,7 @@ def run_backward(do, q, k, v, o, lse, params):
         st[0], st[1], st[2] = _strides3(t)
     with torch.cuda.device(q_.device):
         _lib.bwd(b, torch.cuda.current_stream(q_.device).cuda_stream)
+    del q_, k_, v_, hs, sl, ws  # queued: any reuse of their memory is ordered after the launch
     return dq, dk, dv
 
 
@@ -335,8 +339,18 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
     """attention() on float8 q, k, v ([B, H, S, D] / [B, H_kv, S, D]), all three
     torch.float8_e4m3fn or all three torch.float8_e5m2, with per-tensor descales
     (real = stored * descale); returns bf16 o.  Both products run on the gfx950
-    FP8 matrix path (chia_attn_fwd_fp8); the attention weights are rounded to
-    e4m3 (after scaling by 2^8).  Forward only."""
+    FP8 matrix path (chia_attn_fwd_fp8).  The attention weights P are rounded
+    to e4m3 (round to nearest even) for the P V product, per normaliser:
+      softmax  2^(x - m + 4) with a running max m that moves when a tile's max
+               exceeds it by more than 4, so every weight is <= 2^8; the 2^4
+               factor cancels in the row sum;
+      sigmoid  256 * sigmoid(s + bias), the 256 divided out of o;
+      ReLU     relu(s) clamped to 448 (e4m3's largest value) and unscaled: a
+               score above 448 saturates, a weight below 2^-9 (e4m3's smallest
+               subnormal) becomes 0.  Plain scores (q.k / sqrt(D)) stay far
+               below 448; large softcaps or non-causal ALiBi distances can
+               exceed it.
+    Forward only."""
     _check_fp8(q, k, v, 4)
     B, H, S, D = q.shape
     if (k.shape != v.shape or k.shape[0] != B or k.shape[2:] != q.shape[2:] or k.shape[1] < 1
@@ -578,10 +592,10 @@ def attention_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     if isinstance(q, torch.Tensor) and q.dim() == 3 and q.shape[0] == 0:
         check_cu_seqlens(cu_seqlens, 0, max_seqlen)
         return torch.empty_like(q) if out is None else out
-    a, keep, _, o = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, out, **params)
+    a, keep, qkv, o = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, out, **params)
     with torch.cuda.device(q.device):
         _lib.fwd(a, torch.cuda.current_stream(q.device).cuda_stream)
-    del keep  # the launch is queued; torch's allocator orders any reuse after it on this stream
+    del keep, qkv  # the launch is queued; torch's allocator orders any reuse after it on this stream
     return o
 
 
@@ -610,10 +624,10 @@ def run_forward_varlen(q, k, v, cu_seqlens, max_seqlen, params):
     if T == 0:
         check_cu_seqlens(cu_seqlens, 0, max_seqlen)
         return o, lse
-    a, keep, _, _ = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, o, **params)
+    a, keep, qkv, _ = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, o, **params)
     with torch.cuda.device(q.device):
         _lib.fwd_lse(a, lse.data_ptr() if softmax else 0, torch.cuda.current_stream(q.device).cuda_stream)
-    del keep
+    del keep, qkv  # queued: any reuse of their memory is ordered after the launch
     return o, lse
 
 
@@ -622,7 +636,10 @@ def run_backward_varlen(do, q, k, v, o, lse, cu_seqlens, max_seqlen, params):
     dq, dk, dv = (torch.empty(t.shape, dtype=torch.bfloat16, device=t.device) for t in (q, k, v))
     if q.shape[0] == 0:
         return dq, dk, dv
-    a, keep, _, _ = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, o, **params)
+    # keep (offsets, order, per-head vectors) and qkv (layout copies of q, k, v)
+    # stay referenced until the launch is queued: do_ and the workspace are
+    # allocated below and must not take their memory.
+    a, keep, qkv, _ = _prepare_varlen(q, k, v, cu_seqlens, max_seqlen, o, **params)
     do_ = do if (do.dtype == torch.bfloat16 and _layout_ok_packed(do)) else do.to(torch.bfloat16).contiguous()
     if do_.shape != q.shape:
         raise ValueError(f"do must have q's shape {tuple(q.shape)}, got {tuple(do.shape)}")
@@ -637,7 +654,7 @@ def run_backward_varlen(do, q, k, v, o, lse, cu_seqlens, max_seqlen, params):
         st[0], st[1], st[2] = 0, t.stride(1), t.stride(0)
     with torch.cuda.device(q.device):
         _lib.bwd(b, torch.cuda.current_stream(q.device).cuda_stream)
-    del keep
+    del keep, qkv, ws  # queued: any reuse of their memory is ordered after the launch
     return dq, dk, dv
 
 

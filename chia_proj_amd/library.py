@@ -46,7 +46,10 @@ def fwd(q: Tensor, k: Tensor, v: Tensor, norm: str, causal: bool, window: int, d
     p = _params(norm, causal, window, dilation, block, prefix, scale, head_scale, alibi_slopes, softcap, bias,
                 post_scale)
     o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)  # contiguous, as the fake
-    a, _, _, _, _ = _prepare(q, k, v, o, **p)
+    # Every tensor _prepare returns (layout copies of q, k, v and the per-head
+    # vectors) stays referenced until the launch is queued: a copy freed earlier
+    # would hand its memory to lse while the struct still points at it.
+    a, hs, sl, qkv, _o = _prepare(q, k, v, o, **p)
     B, H, S, _ = q.shape
     if norm == "softmax":
         lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device)
@@ -54,6 +57,7 @@ def fwd(q: Tensor, k: Tensor, v: Tensor, norm: str, causal: bool, window: int, d
         lse = torch.empty(0, dtype=torch.float32, device=q.device)
     with torch.cuda.device(q.device):
         _lib.fwd_lse(a, lse.data_ptr() if lse.numel() else 0, torch.cuda.current_stream(q.device).cuda_stream)
+    del qkv, hs, sl  # queued: torch's allocator orders any reuse after the launch on this stream
     return o, lse
 
 

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import chia_proj_amd  # noqa: F401
-from chia_proj_amd import attention
+from chia_proj_amd import attention, gate
 from oracle.generic import visible_mask
 
 pytestmark = pytest.mark.gpu
@@ -136,3 +136,68 @@ def test_fp8_op_opcheck_and_compile(dtype):
     comp = torch.compile(block, backend="aot_eager", fullgraph=True)(q8, k8, v8, w)
     assert torch.equal(eager, comp)
     assert torch.equal(eager, direct @ w)
+
+
+@pytest.mark.parametrize("norm", ["softmax", "sigmoid"])
+def test_layout_copies_live_through_the_launch(norm):
+    """q, k, v the kernel cannot read in place (unit stride on S, not on D: a
+    [B, H, D, S] tensor viewed .mT) are copied to its layout inside the
+    operators.  Each copy must stay allocated until its launch is queued, so
+    that lse, dO, the gradients and the workspace allocated after it cannot take
+    its memory.  The operator path (autograd) and the packed path are compared
+    with the oracle: o, lse (against a float64 log-sum-exp) and the gradients."""
+    from chia_proj_amd import attention_varlen
+    from chia_proj_amd.attention import _op_forward
+    from oracle.generic import attention_ref
+    from oracle.grad import attention_grad_ref
+
+    _say(f"[lib] layout copies {norm}")
+    B, H, S, D = 2, 2, 320, 64
+    g = torch.Generator("cpu").manual_seed(31)
+    q, k, v, do = (torch.randn(B, H, D, S, generator=g).to(torch.bfloat16).mT for _ in range(4))
+    assert q.stride(-1) != 1
+    kw = dict(norm=norm, causal=True, window=150, bias=-1.0)
+    params = dict(norm=norm, causal=True, window=150, dilation=1, block=0, prefix=0, scale=None, head_scale=None,
+                  alibi_slopes=None, softcap=0.0, bias=-1.0, post_scale=1.0)
+    qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    o, lse = _op_forward(qg, kg, vg, params)
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    ref = attention_ref(q, k, v, **kw)
+    res = gate.north_star_gate(ref, o.detach().float().cpu(), scale_aware=norm != "softmax")
+    assert res.ok, (res.status, res.stats)
+    if norm == "softmax":
+        s = (q.double() @ k.double().transpose(-2, -1)) / math.sqrt(D)
+        ok = visible_mask(S, causal=True, window=150)
+        lref = torch.logsumexp(s.masked_fill(~ok, float("-inf")), -1)
+        assert (lse.double().cpu() - lref).abs().max().item() < 1e-3 * max(1.0, lref.abs().max().item())
+    refs = attention_grad_ref(q, k, v, do, **kw)
+    floor = 1e-3 * max(r.abs().max().item() for r in refs)
+    for label, got, r in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), refs):
+        m = max(r.abs().max().item(), floor)
+        err = (got.float().cpu() - r).abs()
+        assert err.max().item() <= 1e-2 * m and err.mean().item() <= 1e-3 * m, (label, err.max().item(), m)
+
+    # packed: [T, H, D] views with unit stride on T (copied inside), two sequences
+    lens = [200, 120]
+    T = sum(lens)
+    qp, kp, vp, dop = (torch.randn(H, D, T, generator=g).to(torch.bfloat16).permute(2, 0, 1) for _ in range(4))
+    assert qp.stride(-1) != 1
+    cu = torch.tensor([0, lens[0], T], dtype=torch.int32)
+    pg = [t.to(DEV).requires_grad_(True) for t in (qp, kp, vp)]
+    op = attention_varlen(*pg, cu.to(DEV), **kw)
+    op.backward(dop.to(DEV))
+    torch.cuda.synchronize()
+    for b in range(2):
+        a0, a1 = int(cu[b]), int(cu[b + 1])
+        seq = [t[a0:a1].transpose(0, 1).unsqueeze(0) for t in (qp, kp, vp, dop)]
+        r = attention_ref(*seq[:3], **kw)[0]
+        res = gate.north_star_gate(r, op[a0:a1].transpose(0, 1).detach().float().cpu(), scale_aware=norm != "softmax")
+        assert res.ok, (b, res.status, res.stats)
+        refs = attention_grad_ref(*seq, **kw)
+        floor = 1e-3 * max(x.abs().max().item() for x in refs)
+        for label, t, rr in zip(("dq", "dk", "dv"), pg, refs):
+            got = t.grad[a0:a1].transpose(0, 1).unsqueeze(0).float().cpu()
+            m = max(rr.abs().max().item(), floor)
+            err = (got - rr).abs()
+            assert err.max().item() <= 1e-2 * m and err.mean().item() <= 1e-3 * m, (b, label)
