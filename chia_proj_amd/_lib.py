@@ -25,6 +25,7 @@ EXPORTS = (
     "chia_attn_fwd_lse",
     "chia_attn_fwd_fp8",
     "chia_attn_bwd",
+    "chia_attn_bwd_noalloc",
     "chia_attn_bwd_workspace_size",
     "chia_attn_plan",
     "chia_attn_tile_map",
@@ -187,6 +188,8 @@ def _load():
         lib.chia_attn_fwd_fp8.restype = ctypes.c_int
         lib.chia_attn_bwd.argtypes = [ctypes.POINTER(BwdArgs), ctypes.c_void_p]
         lib.chia_attn_bwd.restype = ctypes.c_int
+        lib.chia_attn_bwd_noalloc.argtypes = [ctypes.POINTER(BwdArgs), ctypes.c_void_p]
+        lib.chia_attn_bwd_noalloc.restype = ctypes.c_int
         lib.chia_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
         lib.chia_attn_bwd_workspace_size.restype = ctypes.c_int64
         lib.chia_attn_plan.argtypes = [ctypes.POINTER(AttnArgs), ctypes.POINTER(PlanInfo)]
@@ -249,6 +252,14 @@ def bwd(args: BwdArgs, stream: int) -> None:
     st = _load().chia_attn_bwd(ctypes.byref(args), ctypes.c_void_p(stream))
     if st != 0:
         raise ChiaAttnError(st, "chia_attn_bwd")
+
+
+def bwd_noalloc(args: BwdArgs, stream: int) -> None:
+    """chia_attn_bwd without the workspace: the row statistics go to the library's
+    static per-GPU scratch (calls on one GPU must not overlap)."""
+    st = _load().chia_attn_bwd_noalloc(ctypes.byref(args), ctypes.c_void_p(stream))
+    if st != 0:
+        raise ChiaAttnError(st, "chia_attn_bwd_noalloc")
 
 
 def plan(args: AttnArgs) -> dict:

@@ -7,8 +7,10 @@
 // the caller passes o and every variant parameter explicitly.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 
 #include "attn_fp8_kernel.h"
 #include "chia_attn.h"
@@ -132,6 +134,9 @@ extern "C" const char* chia_attn_status_string(int status) {
     case CHIA_ATTN_ERR_ALIGN: return "tensors must be 16-byte aligned with batch/head/seq strides multiple of 8 elements";
     case CHIA_ATTN_ERR_STRUCT: return "struct_size mismatch or reserved fields not zero";
     case CHIA_ATTN_ERR_WORKSPACE: return "backward workspace NULL or smaller than chia_attn_bwd_workspace_size";
+    case CHIA_ATTN_ERR_SCRATCH:
+      return "chia_attn_bwd_noalloc: the row statistics (chia_attn_bwd_workspace_size bytes) exceed the static "
+             "scratch of CHIA_ATTN_NOALLOC_SCRATCH_BYTES";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -236,7 +241,54 @@ extern "C" int64_t chia_attn_bwd_workspace_size(const chia_attn_args* a) {
   return st != CHIA_ATTN_OK ? st : bwd_workspace(a);
 }
 
-extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
+// ---- allocation-free backward: the row statistics in a static device array -----
+// `scratch` is a file-scope device array: each GPU the library runs on holds its
+// own copy (allocated with the code object, held until the process ends).  In
+// host code its name is only a stand-in for the symbol; the device address is
+// taken once per device with hipGetSymbolAddress, with that device current, and
+// only that address is ever handed to a kernel.
+static __device__ __align__(256) char scratch[CHIA_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (hipGetSymbolAddress on the first
+// call on each device).  Returns a chia_attn_status / hipError_t code.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return (int)err;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  void* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (err != hipSuccess) return (int)err;
+      if (ptr == nullptr) return (int)hipErrorInvalidSymbol;
+      g_scratch[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return CHIA_ATTN_OK;
+}
+
+int launch_bwd(const chia_attn_bwd_args* ba, void* stream, bool noalloc);
+}  // namespace
+
+extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) { return launch_bwd(ba, stream, false); }
+
+extern "C" int chia_attn_bwd_noalloc(const chia_attn_bwd_args* ba, void* stream) {
+  return launch_bwd(ba, stream, true);
+}
+
+namespace {
+// chia_attn_bwd; with `noalloc` the row statistics go to the current device's
+// `scratch` instead of the caller's workspace (whose fields are then ignored).
+int launch_bwd(const chia_attn_bwd_args* ba, void* stream, bool noalloc) {
   if (!ba) return CHIA_ATTN_ERR_NULL;
   if (ba->struct_size != sizeof(chia_attn_bwd_args) || ba->reserved0 != 0) return CHIA_ATTN_ERR_STRUCT;
   for (int i = 0; i < 8; ++i)
@@ -252,15 +304,25 @@ extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
   for (const int64_t* s : {a->q_stride, ba->dout_stride})
     if (s[2] < 0 || s[2] * a->dilation >= kMaxKvRowStride) return CHIA_ATTN_ERR_SHAPE;
   const bool softmax = a->norm == CHIA_ATTN_NORM_SOFTMAX;
+  void* stats = nullptr;
   if (softmax) {
     if (!ba->lse) return CHIA_ATTN_ERR_NULL;
     if ((uintptr_t)ba->lse & 3u) return CHIA_ATTN_ERR_ALIGN;
-    if (!ba->workspace || ba->workspace_bytes < bwd_workspace(a) || ((uintptr_t)ba->workspace & 15u))
-      return CHIA_ATTN_ERR_WORKSPACE;
+    if (noalloc) {
+      if (bwd_workspace(a) > (int64_t)CHIA_ATTN_NOALLOC_SCRATCH_BYTES) return CHIA_ATTN_ERR_SCRATCH;
+    } else {
+      if (!ba->workspace || ba->workspace_bytes < bwd_workspace(a) || ((uintptr_t)ba->workspace & 15u))
+        return CHIA_ATTN_ERR_WORKSPACE;
+      stats = ba->workspace;
+    }
   }
   const int64_t hkv = a->kv_heads > 0 ? a->kv_heads : a->heads;
   const int64_t G = a->heads / hkv;
   if (G > kBwdMaxGroup) return CHIA_ATTN_ERR_SHAPE;
+  if (softmax && noalloc) {
+    const int st_s = scratch_address(&stats);
+    if (st_s != CHIA_ATTN_OK) return st_s;
+  }
 
   BwdParams p;
   std::memset(&p, 0, sizeof(p));
@@ -286,7 +348,7 @@ extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
   p.lse_sb = a->cu_seqlens ? 0 : a->heads * a->seqlen;
   p.lse_sh = a->cu_seqlens ? 1 : a->seqlen;
   p.lse_ss = a->cu_seqlens ? a->heads : 1;
-  p.stats = softmax ? (float*)ba->workspace : nullptr;
+  p.stats = (float*)stats;
   p.head_scale = a->head_scale;
   p.alibi_slopes = a->alibi_slopes;
   p.mask = spec_of(a);
@@ -323,6 +385,7 @@ extern "C" int chia_attn_bwd(const chia_attn_bwd_args* ba, void* stream) {
   if (err == hipSuccess) err = launch(ks.dkdv, g_dkdv, p, s);
   return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
 }
+}  // namespace
 
 extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
   if (!fa) return CHIA_ATTN_ERR_NULL;

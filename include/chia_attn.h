@@ -11,8 +11,9 @@
  *
  * Every entry point takes plain pointers and sizes.  Tensors are bf16 device
  * buffers laid out [batch, heads, seqlen, head_dim] with arbitrary batch/head/
- * seq strides (in elements) and a unit head_dim stride.  The library owns no
- * device memory: the caller allocates q, k, v, o and the per-head vectors.
+ * seq strides (in elements) and a unit head_dim stride.  The caller allocates
+ * q, k, v, o and the per-head vectors; the library's only device memory is the
+ * static scratch array of chia_attn_bwd_noalloc.
  *
  * Reference interface replaced (JoshiP-commits/CHIA_proj):
  *   kernels_gemini31propre_0018/<op>_BEST.py::launch_kernel(q, k, v) -> o
@@ -57,7 +58,8 @@ enum chia_attn_status {
   CHIA_ATTN_ERR_NORM = -6,          /* unknown normaliser                   */
   CHIA_ATTN_ERR_ALIGN = -7,         /* pointer/stride not 16-byte aligned   */
   CHIA_ATTN_ERR_STRUCT = -8,        /* struct_size does not match this ABI  */
-  CHIA_ATTN_ERR_WORKSPACE = -9      /* backward workspace NULL or too small */
+  CHIA_ATTN_ERR_WORKSPACE = -9,     /* backward workspace NULL or too small */
+  CHIA_ATTN_ERR_SCRATCH = -10       /* chia_attn_bwd_noalloc: statistics exceed the static scratch */
 };
 
 typedef struct chia_attn_args {
@@ -173,6 +175,23 @@ int64_t chia_attn_bwd_workspace_size(const chia_attn_args* fwd);
 /* Launch the backward on `stream` (asynchronous; the caller keeps every
  * buffer alive until it completes).  Status codes as chia_attn_fwd. */
 int chia_attn_bwd(const chia_attn_bwd_args* args, void* stream);
+
+/* chia_attn_bwd that allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving or training loops, harnesses that forbid hipMalloc).
+ * The row statistics that chia_attn_bwd keeps in the caller's workspace go to a
+ * static device array of CHIA_ATTN_NOALLOC_SCRATCH_BYTES per GPU instead (held
+ * by each GPU the library runs on until the process ends); the workspace and
+ * workspace_bytes fields are ignored.  A problem whose statistics
+ * (chia_attn_bwd_workspace_size) exceed that size returns
+ * CHIA_ATTN_ERR_SCRATCH before any launch.  Call it with the device of
+ * `stream` current.  Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (other streams, other host threads) race and must
+ * be serialised by the caller.  Nothing in the array needs clearing between
+ * calls (each call writes every statistic it reads).  Results are those of
+ * chia_attn_bwd bit for bit (the same kernels). */
+#define CHIA_ATTN_NOALLOC_SCRATCH_BYTES (8 << 20)
+int chia_attn_bwd_noalloc(const chia_attn_bwd_args* args, void* stream);
 
 /* FP8 forward.  `attn` describes the call as for chia_attn_fwd, with q, k, v
  * pointing at float8 data of one format (`format`: OCP e4m3fn -- 4 exponent

@@ -51,7 +51,7 @@ def test_ctypes_mirrors_header_struct(cname, pyclass):
 
 def test_status_strings_and_version(lib_built):
     assert lib_built.chia_attn_abi_version() == _lib.ABI_VERSION
-    for st in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9):
+    for st in (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10):
         assert _lib.status_string(st)
     assert "unknown" in _lib.status_string(-99)
 
@@ -225,6 +225,23 @@ def test_bwd_rejects_bad_arguments_without_launching(lib_built):
     assert _bwd_status(c, lse=None, workspace=None, workspace_bytes=0, dq=None) == -1
     d = _bwd_ready_args(heads=512, kv_heads=1)       # more than 256 query heads per K/V head
     assert _bwd_status(d) == -2
+
+
+def test_bwd_noalloc_rejects_without_launching(lib_built):
+    """The allocation-free backward checks its arguments as chia_attn_bwd does (the
+    workspace fields aside) and refuses statistics beyond its static scratch."""
+    assert lib_built.chia_attn_bwd_noalloc(None, None) == -1
+    a = _bwd_ready_args()
+    b = _lib.BwdArgs(fwd=ctypes.pointer(a), dout=0x20000, dq=0x30000, dk=0x40000, dv=None, lse=0x60000)
+    assert lib_built.chia_attn_bwd_noalloc(ctypes.byref(b), None) == -1
+    big = _bwd_ready_args(batch=16, heads=16, seqlen=8192)
+    assert lib_built.chia_attn_bwd_workspace_size(ctypes.byref(big)) == 2 * 16 * 16 * 8192 * 4
+    b = _lib.BwdArgs(fwd=ctypes.pointer(big), dout=0x20000, dq=0x30000, dk=0x40000, dv=0x50000, lse=0x60000)
+    for name in ("dout_stride", "dq_stride", "dk_stride", "dv_stride"):
+        st = getattr(b, name)
+        st[0], st[1], st[2] = 4 * 128 * 64, 128 * 64, 64
+    assert lib_built.chia_attn_bwd_noalloc(ctypes.byref(b), None) == -10
+    assert "scratch" in _lib.status_string(-10)
 
 
 def test_fp8_rejects_bad_arguments_without_launching(lib_built):
