@@ -1,7 +1,8 @@
 """CPU checks of chia_proj_amd/csrc/mask.h by brute force: the kernel's
 unclassified fast paths (fast_ranges, wide_range_all) against classify_tile over
 masks, residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp), and
-the multiply-high divider against plain division (tests/cpp/check_udiv.cpp)."""
+the multiply-high divider against plain division (tests/cpp/check_udiv.cpp),
+both built with AddressSanitizer and UndefinedBehaviorSanitizer."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -9,12 +10,13 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
+SANITIZE = ["-g", "-fsanitize=address,undefined", "-fno-sanitize-recover=all"]
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
 def test_fast_ranges_agree_with_classification(tmp_path):
     exe = tmp_path / "check_fast_ranges"
-    subprocess.run(["g++", "-std=c++17", "-O1", f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+    subprocess.run(["g++", "-std=c++17", "-O1", *SANITIZE, f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
                     str(ROOT / "tests" / "cpp" / "check_fast_ranges.cpp"), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
@@ -24,7 +26,7 @@ def test_fast_ranges_agree_with_classification(tmp_path):
 @pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
 def test_udiv_matches_division(tmp_path):
     exe = tmp_path / "check_udiv"
-    subprocess.run(["g++", "-std=c++17", "-O2", f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+    subprocess.run(["g++", "-std=c++17", "-O1", *SANITIZE, f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
                     str(ROOT / "tests" / "cpp" / "check_udiv.cpp"), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
