@@ -23,7 +23,7 @@ LIB_PATH = PKG_DIR / LIB_NAME
 BUILD_DIR = REPO_DIR / "_build"
 
 SOURCES = ["attn_fwd_d64.hip", "attn_fwd_d128.hip", "attn_bwd_d64.hip", "attn_bwd_d128.hip", "attn_fp8.hip", "attn_api.hip"]
-HEADERS = ["attn_fwd_kernel.h", "mask.h"]
+HEADERS = ["attn_fwd_kernel.h", "lds_layout.h", "mask.h"]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [

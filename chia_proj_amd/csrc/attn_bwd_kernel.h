@@ -171,7 +171,9 @@ __device__ __forceinline__ ScoreGrad<NORM, ALIBI, SOFTCAP> score_consts(const Bw
 
 // One 64-row tile of a [S, D] bf16 tensor (row stride rs elements, rows from
 // `row` of the residue's sub-sequence, clamped to S - 1) into LDS at `dst`:
-// row r, 16-byte chunk c lands in slot c ^ (r & 7).  Wavefront w of NW moves
+// row r, 16-byte chunk c lands in slot k_slot<D>(r, c), which keeps both the
+// row reads and the transposed reads of the tile free of bank conflicts.
+// Wavefront w of NW moves
 // chunks [(n NW + w) 64, +64) for n < NDMA.
 template <int D, int NW>
 __device__ __forceinline__ void dma_rows(const uint16_t* base, int64_t rs, int row, int S, char* dst, int wave,
@@ -184,7 +186,7 @@ __device__ __forceinline__ void dma_rows(const uint16_t* base, int64_t rs, int r
     const int pos = (n * NW + wave) * 64 + lane;
     const int r = pos / DQ, slot = pos % DQ;
     const int rr = imin32(r, S - 1 - row);
-    dma16s(src, (uint32_t)(2 * ((int64_t)rr * rs + 8 * k_slot(r, slot))), lds_addr(dst + (n * NW + wave) * 1024));
+    dma16s(src, (uint32_t)(2 * ((int64_t)rr * rs + 8 * k_slot<D>(r, slot))), lds_addr(dst + (n * NW + wave) * 1024));
   }
 }
 
@@ -307,10 +309,11 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
     for (int e = 0; e < 16; ++e) dq[db][e] = 0.f;
 
   // LDS lane offsets: row reads (A = K or V rows) and transposed reads (A = K^T)
-  const int k_lane = lq * RP + 16 * k_slot(lq, lh);
+  const int k_lane = lq * RP + 16 * k_slot<D>(lq, lh);
   const int g16 = lane >> 4, s16 = lane & 15;
   const int t_row = 4 * (g16 >> 1) + (s16 >> 2);
-  const int t_lane = t_row * RP + 16 * ((2 * (g16 & 1) + ((s16 & 3) >> 1)) ^ t_row) + 8 * (s16 & 1);
+  const int t_lane = t_row * RP + 16 * k_slot<D>(t_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
+  const int t_lane8 = (t_lane ^ (16 * row_swz<D>(8))) + 8 * RP;  // the same lanes 8 rows down
 
   auto issue = [&](int it) {
     const int jt0 = tile_at(tr, it) * BN;
@@ -369,9 +372,9 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
       const int kb = c >> 1, half = c & 1;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const char* ka = St + 16 * c * RP + (t_lane ^ (64 * db));
-        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)ka);
-        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(ka + 8 * RP));
+        const char* ka = St + 16 * c * RP;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(ka + (t_lane ^ (64 * db))));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(ka + (t_lane8 ^ (64 * db))));
         const bf16x8_t a = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         const u32x4_t wv = {pk[kb][4 * half], pk[kb][4 * half + 1], pk[kb][4 * half + 2], pk[kb][4 * half + 3]};
         dq[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, __builtin_bit_cast(bf16x8_t, wv), dq[db], 0, 0, 0);
@@ -476,10 +479,11 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
 #pragma unroll
     for (int e = 0; e < 16; ++e) dk[db][e] = dv[db][e] = 0.f;
 
-  const int k_lane = lq * RP + 16 * k_slot(lq, lh);
+  const int k_lane = lq * RP + 16 * k_slot<D>(lq, lh);
   const int g16 = lane >> 4, s16 = lane & 15;
   const int t_row = 4 * (g16 >> 1) + (s16 >> 2);
-  const int t_lane = t_row * RP + 16 * ((2 * (g16 & 1) + ((s16 & 3) >> 1)) ^ t_row) + 8 * (s16 & 1);
+  const int t_lane = t_row * RP + 16 * k_slot<D>(t_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
+  const int t_lane8 = (t_lane ^ (16 * row_swz<D>(8))) + 8 * RP;  // the same lanes 8 rows down
 
   // Tiles run row tile t_lo .. t_lo + n_qt - 1 of query head hkv G, then of the
   // next head of the group.  Two cursors walk them (the DMA one runs ahead);
@@ -596,12 +600,13 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
         const int c = 2 * qb + half;
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const char* qa = St + 16 * c * RP + (t_lane ^ (64 * db));
-          const char* da = St + T_BYTES + 16 * c * RP + (t_lane ^ (64 * db));
-          const i16x4_t qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)qa);
-          const i16x4_t qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(qa + 8 * RP));
-          const i16x4_t dlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)da);
-          const i16x4_t dhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(da + 8 * RP));
+          const char* qa = St + 16 * c * RP;
+          const char* da = St + T_BYTES + 16 * c * RP;
+          const int lo_off = t_lane ^ (64 * db), hi_off = t_lane8 ^ (64 * db);
+          const i16x4_t qlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(qa + lo_off));
+          const i16x4_t qhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(qa + hi_off));
+          const i16x4_t dlo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(da + lo_off));
+          const i16x4_t dhi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(da + hi_off));
           const bf16x8_t aq = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(qlo, qhi, 0, 1, 2, 3, 4, 5, 6, 7));
           const bf16x8_t ado = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(dlo, dhi, 0, 1, 2, 3, 4, 5, 6, 7));
           const u32x4_t wp = {pp[4 * half], pp[4 * half + 1], pp[4 * half + 2], pp[4 * half + 3]};

@@ -44,10 +44,10 @@
 //     k0..k0+3 of column d0 + i -- exactly the key order of the B operand.
 //   LDS tiles are dense rows of 2D bytes whose 16-byte chunks are XOR-swizzled
 //   (a DMA load fills 1 KB contiguously, so rows cannot be padded): K chunk c
-//   of row r sits in slot c ^ (r & 7), so the eight rows of a ds_read_b128
-//   phase hit distinct bank groups; V chunk c sits in slot c ^ 2 (r & 3), so
-//   the four rows x 32 bytes of one transposed-read group do.  With rows of
-//   a multiple of 128 bytes every fragment offset is a per-lane base XOR a
+//   of row r sits in slot k_slot(r, c), so the 16 rows of a ds_read_b128 pass
+//   hit distinct bank groups; V chunk c sits in slot v_slot(r, c), so the
+//   four rows x 64 bytes of one 32-lane transposed-read pass do.  With rows
+//   of a multiple of 128 bytes every fragment offset is a per-lane base XOR a
 //   compile-time constant.
 //   The softmax runs per tile in the exp2 domain with a lazily moved
 //   reference max: the running max (and the O / l rescale) only changes when
@@ -58,6 +58,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "lds_layout.h"
 #include "mask.h"
 
 namespace chia {
@@ -167,10 +168,6 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
   const uint64_t u = ((uint64_t)hi << 32) | (uint64_t)lo;
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(u), "{m0}"(lds_base) : "memory");
 }
-
-// Swizzled 16-byte slot of chunk c of row r in the K and V tiles.
-__device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 7); }
-__device__ __forceinline__ int v_slot(int r, int c) { return c ^ (2 * (r & 3)); }
 
 // Hardware dispatches workgroup x to XCD x % 8.  Renumber so each XCD runs a
 // contiguous range of logical workgroups (the query blocks of the same heads
@@ -379,8 +376,8 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   for (int n = 0; n < NDMA; ++n) {
     const int pos = (n * NW + wave) * 64 + lane;
     const int row = pos / DQ, slot = pos % DQ;
-    k_dma[n] = (uint32_t)(2 * ((int64_t)row * krs + 8 * k_slot(row, slot)));
-    v_dma[n] = (uint32_t)(2 * ((int64_t)row * vrs + 8 * v_slot(row, slot)));
+    k_dma[n] = (uint32_t)(2 * ((int64_t)row * krs + 8 * k_slot<D>(row, slot)));
+    v_dma[n] = (uint32_t)(2 * ((int64_t)row * vrs + 8 * v_slot<D>(row, slot)));
   }
   auto issue_tile = [&](int jt0, int stage) {
     char* kst = lds + stage * STAGE_BYTES;
@@ -400,8 +397,8 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
         const int row = pos / DQ, slot = pos % DQ;
         const int rr = imin32(row, g.S - 1 - jt0);
         const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
-        dma16s(kt, (uint32_t)(2 * ((int64_t)rr * krs + 8 * k_slot(row, slot))), lbase);
-        dma16s(vt, (uint32_t)(2 * ((int64_t)rr * vrs + 8 * v_slot(row, slot))), lbase + K_BYTES);
+        dma16s(kt, (uint32_t)(2 * ((int64_t)rr * krs + 8 * k_slot<D>(row, slot))), lbase);
+        dma16s(vt, (uint32_t)(2 * ((int64_t)rr * vrs + 8 * v_slot<D>(row, slot))), lbase + K_BYTES);
       }
     }
   };
@@ -491,13 +488,13 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 
   // Per-lane LDS byte offsets.  K fragment (kb, kk): row 32 kb + lq, chunk
   // 2 kk + lh -> byte (32 kb) RP + [k_lane ^ 32 kk].
-  const int k_lane = lq * RP + 16 * k_slot(lq, lh);
+  const int k_lane = lq * RP + 16 * k_slot<D>(lq, lh);
   // V transposed read (c, rr, db): lane (group g16, slot s16) addresses row
   // 16 c + 8 rr + 4 (g16 / 2) + s16 / 4 and elements 32 db + 16 (g16 % 2) +
   // 4 (s16 % 4) .. +3, i.e. byte (16 c + 8 rr) RP + [v_lane ^ 64 db].
   const int g16 = lane >> 4, s16 = lane & 15;
   const int v_row = 4 * (g16 >> 1) + (s16 >> 2);
-  const int v_lane = K_BYTES + v_row * RP + 16 * v_slot(v_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
+  const int v_lane = K_BYTES + v_row * RP + 16 * v_slot<D>(v_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
 
   // One tile for this wavefront, as a set of 32 x 32 score blocks ("streams"):
   //   PAIR (WIDE = false): four streams, query blocks {0, 1} x key blocks

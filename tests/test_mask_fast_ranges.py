@@ -1,8 +1,9 @@
 """CPU checks of chia_proj_amd/csrc/mask.h by brute force: the kernel's
 unclassified fast paths (fast_ranges, wide_range_all) against classify_tile over
 masks, residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp), and
-the multiply-high divider against plain division (tests/cpp/check_udiv.cpp),
-both built with AddressSanitizer and UndefinedBehaviorSanitizer."""
+the multiply-high divider against plain division (tests/cpp/check_udiv.cpp) and
+the LDS tile layout against a bank model (tests/cpp/check_lds_banks.cpp), all
+built with AddressSanitizer and UndefinedBehaviorSanitizer."""
 import shutil
 import subprocess
 from pathlib import Path
@@ -31,3 +32,15 @@ def test_udiv_matches_division(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "pairs" in out.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_lds_layout_is_bank_conflict_free(tmp_path):
+    """The LDS chunk placement (csrc/lds_layout.h) against a 64-bank model that
+    reproduces the conflict counters measured on the layout it replaced."""
+    exe = tmp_path / "check_lds_banks"
+    subprocess.run(["g++", "-std=c++17", "-O1", *SANITIZE, f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+                    str(ROOT / "tests" / "cpp" / "check_lds_banks.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "0 failures" in out.stdout
