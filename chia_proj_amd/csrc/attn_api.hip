@@ -19,7 +19,8 @@ namespace chia {
 
 using KernelFn = void (*)(FwdParams);
 KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
-KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap);
+KernelFn select_kernel_d128(int norm);
+KernelFn select_q1_kernel_d128(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d128(int norm, bool alibi, bool softcap);
 Fp8KernelFn select_fp8_kernel(int head_dim, int format, int norm, bool alibi, bool softcap);
@@ -81,20 +82,38 @@ constexpr int kCUs = 256;  // MI355X compute units
 // the same work.
 bool zigzag_of(const MaskSpec& m) { return m.lo >= 0 && m.hi >= kInf && m.blk == 0; }
 
+// Score path of a forward call: the kernel instantiation's ALiBi / softcap
+// switches.  The plain sigmoid kernel takes the bias as the factor
+// 2^(-bias log2 e), which must be a normal float; a larger |bias| runs the
+// general score path (the ALiBi kernel with null, i.e. zero, slopes).
+struct ScorePath {
+  bool alibi, softcap;
+};
+ScorePath score_path_of(const chia_attn_args* a) {
+  ScorePath sp{a->alibi_slopes != nullptr, a->softcap > 0.f};
+  if (a->norm == CHIA_ATTN_NORM_SIGMOID && !sp.alibi && !sp.softcap && !(std::fabs(-a->bias * kLog2e) <= 120.f))
+    sp.alibi = true;
+  return sp;
+}
+
 // Launch geometry shared by chia_attn_fwd and the planner.
 struct Geometry {
   int waves;       // wavefronts per workgroup
   int rows;        // rows per row block (32 per wavefront)
-  int n_pairs;     // row-block pairs per (b, h, residue 0)
+  int n_pairs;     // workgroups per (b, h, residue 0): row-block pairs, or
+                   // for the one-block core without pairing, row blocks
   int residues;
   int zigzag;
+  bool q1;         // the head_dim 128 one-block core (attn_fwd_q1_kernel.h)
   int64_t workgroups;
 };
 
-Geometry geometry_of(const MaskSpec& m, int64_t batch, int64_t heads) {
+// The paired core: a workgroup owns two row blocks.
+Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
   Geometry geo;
   geo.residues = num_residues(m);
   geo.zigzag = zigzag_of(m) ? 1 : 0;
+  geo.q1 = false;
   const int32_t s0 = residue_geom(m, 0).S;  // longest residue class
   // 4 wavefronts share each K/V tile among more rows; fall back to 2 when
   // that leaves fewer than two workgroups per CU.  Windowed or block masks
@@ -110,6 +129,27 @@ Geometry geometry_of(const MaskSpec& m, int64_t batch, int64_t heads) {
     geo.workgroups = batch * heads * geo.residues * geo.n_pairs;
     if (geo.workgroups >= 2 * kCUs) break;
   }
+  return geo;
+}
+
+// The forward's core and geometry.  Head dim 64: the paired core.  Head dim
+// 128: the one-block core (two wavefronts per SIMD), except on full rows
+// (no causal pairing, window or block) of 4096 keys or more without a score
+// modifier and with two 4-wavefront workgroups per CU, where the paired
+// core's pipelined run and its K/V tiles shared by two row blocks measured
+// faster (B4 H16 S4096: sigmoid 504 vs 533 us, ReLU 447 vs 465 us).
+Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const ScorePath& sp) {
+  Geometry geo = paired_geometry(m, a->batch, a->heads);
+  if (a->head_dim != 128) return geo;
+  const bool banded = m.hi < kInf || m.blk > 0;
+  const int32_t s0 = residue_geom(m, 0).S;
+  if (!geo.zigzag && !banded && s0 >= 4096 && !sp.alibi && !sp.softcap && geo.waves == 4) return geo;
+  geo.q1 = true;
+  geo.waves = 4;
+  geo.rows = 128;
+  const int64_t nblk = (s0 + geo.rows - 1) / geo.rows;
+  geo.n_pairs = (int)(geo.zigzag ? (nblk + 1) / 2 : nblk);
+  geo.workgroups = a->batch * a->heads * geo.residues * geo.n_pairs;
   return geo;
 }
 
@@ -170,7 +210,8 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   p.lse_sb = a->cu_seqlens ? 0 : a->heads * a->seqlen;
   p.lse_sh = a->cu_seqlens ? 1 : a->seqlen;
   p.lse_ss = a->cu_seqlens ? a->heads : 1;
-  const Geometry geo = geometry_of(p.mask, a->batch, a->heads);
+  const ScorePath sp = score_path_of(a);
+  const Geometry geo = forward_geometry(a, p.mask, sp);
   p.residues = geo.residues;
   p.n_pairs = geo.n_pairs;
   p.zigzag = geo.zigzag;
@@ -187,15 +228,9 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   p.post_scale = a->post_scale;
   p.lse = a->norm == CHIA_ATTN_NORM_SOFTMAX ? lse : nullptr;
 
-  bool alibi = a->alibi_slopes != nullptr;
-  const bool softcap = a->softcap > 0.f;
-  // The plain sigmoid kernel takes the bias as the factor 2^(-bias log2 e),
-  // which must be a normal float; a larger |bias| runs the general score path
-  // (the ALiBi kernel with null slopes, i.e. zero).
-  if (a->norm == CHIA_ATTN_NORM_SIGMOID && !alibi && !softcap && !(std::fabs(-a->bias * kLog2e) <= 120.f))
-    alibi = true;
-  KernelFn fn = a->head_dim == 64 ? select_kernel_d64(waves, (int)a->norm, alibi, softcap)
-                                  : select_kernel_d128(waves, (int)a->norm, alibi, softcap);
+  KernelFn fn = a->head_dim == 64 ? select_kernel_d64(waves, (int)a->norm, sp.alibi, sp.softcap)
+               : geo.q1            ? select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap)
+                                   : select_kernel_d128((int)a->norm);
   void* kargs[] = {&p};
   hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(64 * waves), kargs,
                                    0, (hipStream_t)stream);
@@ -450,12 +485,14 @@ extern "C" int chia_attn_plan(const chia_attn_args* a, chia_attn_plan_info* out)
   if (!out) return CHIA_ATTN_ERR_NULL;
   std::memset(out, 0, sizeof(*out));
   const MaskSpec spec = spec_of(a);
-  const Geometry geo = geometry_of(spec, a->batch, a->heads);
+  const Geometry geo = forward_geometry(a, spec, score_path_of(a));
   const int bn = kBN;
   const int64_t bhn = a->batch * a->heads;
-  out->block_m = 2 * geo.rows;  // rows per workgroup (two row blocks)
-  out->block_n = bn;
-  out->wave_m = 32;             // visited-tile unit: 32 rows x block_n keys
+  // The paired core computes two row blocks per KV tile in 32 x 64 sub-tiles;
+  // the one-block core one row block per KV tile, in 32-key steps.
+  out->block_m = geo.q1 ? geo.rows : 2 * geo.rows;  // rows per workgroup step
+  out->block_n = geo.q1 ? bn / 2 : bn;                // keys per computed step
+  out->wave_m = 32;  // visited-tile unit: 32 rows x block_n keys
   out->waves = geo.waves;
   out->residues = geo.residues;
   out->workgroups = geo.workgroups;
@@ -465,34 +502,56 @@ extern "C" int chia_attn_plan(const chia_attn_args* a, chia_attn_plan_info* out)
     if (g.S <= 0) continue;
     const int64_t nkt = (g.S + bn - 1) / bn;
     const int nblk = (g.S + geo.rows - 1) / geo.rows;
-    tiles_total += (int64_t)((nblk + 1) / 2) * nkt;
-    for (int pr = 0; pr < geo.n_pairs; ++pr) {
-      int b0, b1;
-      if (geo.zigzag) {
-        b0 = pr;
-        b1 = nblk - 1 - pr;
-        if (b1 < b0) continue;
-        if (b1 == b0) b1 = -1;
-      } else {
-        b0 = 2 * pr;
-        b1 = 2 * pr + 1;
-        if (b0 >= nblk) continue;
-        if (b1 >= nblk) b1 = -1;
-      }
-      const int32_t hull_hi = imin32((b1 >= 0 ? b1 : b0) * geo.rows + geo.rows - 1, g.S - 1);
-      const TileRange tr = tile_range(g, b0 * geo.rows, hull_hi, bn);
-      const int n = tr.n_pre + tr.n2;
-      tiles_visited += n;
-      for (int it = 0; it < n; ++it) {
-        const int32_t jt0 = tile_at(tr, it) * bn;
-        for (int blk : {b0, b1}) {
-          if (blk < 0) continue;
+    if (geo.q1) {
+      // every row block once (by its workgroup), its own key range, 32-key
+      // steps a wavefront skips when none of its rows sees them
+      tiles_total += (int64_t)nblk * 2 * nkt;
+      for (int blk = 0; blk < nblk; ++blk) {
+        const TileRange tr = tile_range(g, blk * geo.rows, imin32(blk * geo.rows + geo.rows - 1, g.S - 1), bn);
+        const int n = tr.n_pre + tr.n2;
+        tiles_visited += 2 * n;
+        for (int it = 0; it < n; ++it)
           for (int w = 0; w < geo.waves; ++w) {
             const int32_t r0 = blk * geo.rows + 32 * w;
             if (r0 >= g.S) continue;
-            const int cls = classify_tile(g, r0, imin32(r0 + 31, g.S - 1), jt0, jt0 + bn - 1);
-            if (cls != TILE_EMPTY) ++wave_tiles;
-            if (cls == TILE_PARTIAL) ++wave_partial;
+            for (int kb = 0; kb < 2; ++kb) {
+              const int32_t c = tile_at(tr, it) * bn + 32 * kb;
+              const int cls = classify_tile(g, r0, imin32(r0 + 31, g.S - 1), c, c + 31);
+              if (cls != TILE_EMPTY) ++wave_tiles;
+              if (cls == TILE_PARTIAL) ++wave_partial;
+            }
+          }
+      }
+    } else {
+      tiles_total += (int64_t)((nblk + 1) / 2) * nkt;
+      for (int pr = 0; pr < geo.n_pairs; ++pr) {
+        int b0, b1;
+        if (geo.zigzag) {
+          b0 = pr;
+          b1 = nblk - 1 - pr;
+          if (b1 < b0) continue;
+          if (b1 == b0) b1 = -1;
+        } else {
+          b0 = 2 * pr;
+          b1 = 2 * pr + 1;
+          if (b0 >= nblk) continue;
+          if (b1 >= nblk) b1 = -1;
+        }
+        const int32_t hull_hi = imin32((b1 >= 0 ? b1 : b0) * geo.rows + geo.rows - 1, g.S - 1);
+        const TileRange tr = tile_range(g, b0 * geo.rows, hull_hi, bn);
+        const int n = tr.n_pre + tr.n2;
+        tiles_visited += n;
+        for (int it = 0; it < n; ++it) {
+          const int32_t jt0 = tile_at(tr, it) * bn;
+          for (int blk : {b0, b1}) {
+            if (blk < 0) continue;
+            for (int w = 0; w < geo.waves; ++w) {
+              const int32_t r0 = blk * geo.rows + 32 * w;
+              if (r0 >= g.S) continue;
+              const int cls = classify_tile(g, r0, imin32(r0 + 31, g.S - 1), jt0, jt0 + bn - 1);
+              if (cls != TILE_EMPTY) ++wave_tiles;
+              if (cls == TILE_PARTIAL) ++wave_partial;
+            }
           }
         }
       }

@@ -1,32 +1,19 @@
-// attn_fwd_d128.hip -- instantiations of the forward core for head_dim 128:
-// {2, 4} wavefronts per workgroup x 3 normalisers x ALiBi on/off x softcap
-// on/off.  Split by head dim so the two halves compile in parallel.
+// attn_fwd_d128.hip -- instantiations of the paired forward core for head_dim
+// 128.  The dispatcher runs it only on full rows of 4096 keys or more without
+// a score modifier, with 4 wavefronts per workgroup (every other head_dim
+// 128 forward runs the one-block core, attn_fwd_q1_d128.hip): the three
+// normalisers.
 #include "attn_fwd_kernel.h"
 
 namespace chia {
 
 using KernelFn = void (*)(FwdParams);
 
-template <int NW, int NORM, bool AL, bool SC>
-static KernelFn inst() {
-  return attn_fwd_kernel<128, NW, NORM, AL, SC>;
-}
-
-template <int NW>
-static KernelFn pick(int norm, bool alibi, bool softcap) {
-  static const KernelFn table[3][2][2] = {
-      {{inst<NW, NORM_SOFTMAX, false, false>(), inst<NW, NORM_SOFTMAX, false, true>()},
-       {inst<NW, NORM_SOFTMAX, true, false>(), inst<NW, NORM_SOFTMAX, true, true>()}},
-      {{inst<NW, NORM_SIGMOID, false, false>(), inst<NW, NORM_SIGMOID, false, true>()},
-       {inst<NW, NORM_SIGMOID, true, false>(), inst<NW, NORM_SIGMOID, true, true>()}},
-      {{inst<NW, NORM_RELU, false, false>(), inst<NW, NORM_RELU, false, true>()},
-       {inst<NW, NORM_RELU, true, false>(), inst<NW, NORM_RELU, true, true>()}},
-  };
-  return table[norm][alibi ? 1 : 0][softcap ? 1 : 0];
-}
-
-KernelFn select_kernel_d128(int waves, int norm, bool alibi, bool softcap) {
-  return waves == 2 ? pick<2>(norm, alibi, softcap) : pick<4>(norm, alibi, softcap);
+KernelFn select_kernel_d128(int norm) {
+  static const KernelFn table[3] = {attn_fwd_kernel<128, 4, NORM_SOFTMAX, false, false>,
+                                    attn_fwd_kernel<128, 4, NORM_SIGMOID, false, false>,
+                                    attn_fwd_kernel<128, 4, NORM_RELU, false, false>};
+  return table[norm];
 }
 
 }  // namespace chia

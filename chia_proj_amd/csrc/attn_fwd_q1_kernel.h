@@ -1,0 +1,426 @@
+// attn_fwd_q1_kernel.h -- the head_dim 128 forward core: one 32-row query
+// block per wavefront, two wavefronts per SIMD.
+//
+// Reference semantics: the eager closures of extra_bench.py:32-62 and
+// sigmoid_fix.py:34-40, as for attn_fwd_kernel.h, whose helpers (DMA, LDS
+// layout, score constants, masks, packing) this kernel shares.
+//
+// Why a second core: at head_dim 128 the paired core (two query blocks per
+// wavefront) holds 128 accumulator registers of O alone and runs one
+// wavefront per SIMD, so nothing hides its softmax behind another
+// wavefront's MFMAs.  One query block per wavefront needs ~180 VGPRs (no
+// spills), two wavefronts fit on each SIMD, and the SIMD interleaves them.
+// The paired core keeps the case where it measured faster: full rows
+// (no causal pairing, window or block) of 4096 keys or more, where sharing
+// each K/V tile between two row blocks halves the K/V reads.
+//
+// Work decomposition
+//   * a workgroup of 4 wavefronts owns row blocks of 128 rows of one (batch,
+//     head, dilation residue); each wavefront owns 32 of them (one query
+//     block, ONE MFMA stream);
+//   * for a causal band without a window (zigzag), a workgroup processes
+//     block i and then block n-1-i, one after the other, so every workgroup
+//     does the same work; otherwise one block;
+//   * the K / V tiles (64 keys) of the block's key range go HBM -> LDS with
+//     global_load_lds_dwordx4 through NS stages (one barrier per tile); the
+//     DMA runs across the boundary between the two blocks of a pair;
+//   * a tile is computed as two 32-key steps: S^T = K Q^T (8 MFMAs), score
+//     modifier, mask on partial steps, normaliser with its own row-max
+//     update, then O^T += V^T P^T (8 MFMAs), with the matrix-core layouts of
+//     the paired core (lane = query column; V^T read with
+//     ds_read_b64_tr_b16); a 32-key step no row of the wavefront sees is
+//     skipped.
+#pragma once
+#include "attn_fwd_kernel.h"
+
+namespace chia {
+
+// Waves per SIMD the register budget targets, and LDS stages per workgroup
+// (two workgroups per CU x 2 stages x 32 KB at head_dim 128).
+template <int D>
+struct Q1Config {
+  static_assert(D == 128, "the one-block core is built for head_dim 128");
+  static constexpr int occupancy = 2;
+  static constexpr int stages = 2;
+};
+
+template <int D, int NORM, bool ALIBI, bool SOFTCAP>
+__global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kernel(const FwdParams p) {
+  constexpr int NW = 4;
+  constexpr int BN = kBN;
+  constexpr int NT = NW * 64;
+  constexpr int BM = NW * 32;          // rows per block
+  constexpr int DK = D / 16;           // k-steps of the QK^T MFMA
+  constexpr int DB = D / 32;           // 32-row d blocks of O^T
+  constexpr int DQ = D / 8;            // 16-byte chunks per K/V row
+  constexpr int RP = 2 * D;            // LDS row pitch (bytes)
+  constexpr int NDMA = BN * DQ / NT;   // 1 KB DMA loads per wavefront per tile (each of K, V)
+  constexpr int K_BYTES = BN * RP;
+  constexpr int STAGE_BYTES = 2 * K_BYTES;
+  constexpr int NS = Q1Config<D>::stages;
+  static_assert(NDMA >= 1 && BN * DQ % NT == 0, "tile does not split into whole DMA loads");
+  static_assert(RP % 128 == 0, "rows must be whole multiples of 128 bytes for the XOR offsets");
+  static_assert(DB % 2 == 0, "d-blocks are read in pairs");
+  constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
+  constexpr bool kBiasInit = ALIBI && !SOFTCAP;
+  constexpr bool kScaledSoftmax = kPlainSoftmax || (kBiasInit && NORM == NORM_SOFTMAX);
+  constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
+  constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
+  constexpr bool kSigFold = NORM == NORM_SIGMOID && !ALIBI && !SOFTCAP;
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, lh = lane >> 5;
+
+  // ---- workgroup -> (batch, head, residue, unit) ----------------------------
+  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
+  const int bhr = udiv(L, p.div_pairs);
+  const int pr = L - bhr * p.n_pairs;
+  const int bh = udiv(bhr, p.div_res);
+  const int r = bhr - bh * p.residues;
+  const int bs = udiv(bh, p.div_h);
+  const int h = bh - bs * p.H;
+  const int b = seq_of(p.seq_order, bs);
+  const SeqSpan seq = seq_span(p.cu_seqlens, b, p.mask.S);
+  MaskSpec ms = p.mask;
+  ms.S = seq.len;
+  const MaskGeom g = residue_geom(ms, r);
+  const int nblk = (g.S + BM - 1) / BM;
+  int blk0, blk1;
+  if (p.zigzag) {
+    blk0 = pr;
+    blk1 = nblk - 1 - pr;
+    if (blk1 < blk0) return;  // whole workgroup, before any barrier
+    if (blk1 == blk0) blk1 = -1;
+  } else {
+    blk0 = pr;
+    blk1 = -1;
+    if (blk0 >= nblk) return;
+  }
+
+  const int dil = p.mask.dil;
+  const int64_t t0 = seq.tok0 + r;
+  const uint16_t* qh = p.q + b * p.q_sb + h * p.q_sh + t0 * p.q_ss;
+  const int hk = udiv(h, p.div_group);
+  const uint16_t* kh = p.k + b * p.k_sb + hk * p.k_sh + t0 * p.k_ss;
+  const uint16_t* vh = p.v + b * p.v_sb + hk * p.v_sh + t0 * p.v_ss;
+  uint16_t* oh = p.o + b * p.o_sb + h * p.o_sh + t0 * p.o_ss;
+  const int64_t qrs = p.q_ss * dil, krs = p.k_ss * dil, vrs = p.v_ss * dil, ors = p.o_ss * dil;
+
+  // ---- per-head score constants (as in attn_fwd_kernel) ----------------------
+  const float hs = p.head_scale ? p.head_scale[h] : 1.0f;
+  const float slope = ALIBI && p.alibi_slopes ? p.alibi_slopes[h] : 0.0f;
+  const float c1 = p.scale * hs;
+  const float sl = slope * (float)dil;
+  float kq, ks, k0 = 0.f, sc_a = 0.f, sc_b = 0.f;
+  if constexpr (SOFTCAP) {
+    const float f = 2.0f * kLog2e / p.softcap;
+    kq = c1 * f;
+    ks = sl * f;
+    if constexpr (NORM == NORM_SOFTMAX) {
+      sc_a = -2.0f * p.softcap * kLog2e;
+      sc_b = p.softcap * kLog2e;
+    } else if constexpr (NORM == NORM_SIGMOID) {
+      sc_a = 2.0f * p.softcap * kLog2e;
+      sc_b = -(p.softcap + p.bias) * kLog2e;
+    } else {
+      sc_a = -2.0f * p.softcap;
+      sc_b = p.softcap;
+    }
+  } else if constexpr (NORM == NORM_SOFTMAX) {
+    kq = c1 * kLog2e;
+    ks = sl * kLog2e;
+  } else if constexpr (NORM == NORM_SIGMOID) {
+    kq = -c1 * kLog2e;
+    ks = -sl * kLog2e;
+    k0 = -p.bias * kLog2e;
+  } else {
+    kq = ALIBI ? c1 : 1.0f;
+    ks = sl;
+  }
+  const float post = kRawRelu ? p.post_scale * c1 : p.post_scale;
+  const float bq = kBiasInit ? sl / c1 : 0.f;
+  const float sig_c =
+      kSigFold ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__builtin_amdgcn_exp2f(k0)))) : 0.f;
+
+  // ---- the workgroup's steps: the tiles of block 0, then those of block 1 -----
+  const TileRange tr0 = tile_range(g, blk0 * BM, imin32(blk0 * BM + BM - 1, g.S - 1), BN);
+  const int n0 = tr0.n_pre + tr0.n2;
+  TileRange tr1{0, 0, 0};
+  if (blk1 >= 0) tr1 = tile_range(g, blk1 * BM, imin32(blk1 * BM + BM - 1, g.S - 1), BN);
+  const int nsteps = n0 + tr1.n_pre + tr1.n2;
+  auto step_key0 = [&](int s) { return (s < n0 ? tile_at(tr0, s) : tile_at(tr1, s - n0)) * BN; };
+
+  uint32_t k_dma[NDMA], v_dma[NDMA];
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int pos = (n * NW + wave) * 64 + lane;
+    const int row = pos / DQ, slot = pos % DQ;
+    k_dma[n] = (uint32_t)(2 * ((int64_t)row * krs + 8 * k_slot<D>(row, slot)));
+    v_dma[n] = (uint32_t)(2 * ((int64_t)row * vrs + 8 * v_slot<D>(row, slot)));
+  }
+  auto issue_step = [&](int s) {
+    const int jt0 = step_key0(s);
+    char* kst = lds + (s % NS) * STAGE_BYTES;
+    const uint16_t* kt = kh + (int64_t)jt0 * krs;
+    const uint16_t* vt = vh + (int64_t)jt0 * vrs;
+    if (jt0 + BN <= g.S) {
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) {
+        const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
+        dma16s(kt, k_dma[n], lbase);
+        dma16s(vt, v_dma[n], lbase + K_BYTES);
+      }
+    } else {
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) {
+        const int pos = (n * NW + wave) * 64 + lane;
+        const int row = pos / DQ, slot = pos % DQ;
+        const int rr = imin32(row, g.S - 1 - jt0);
+        const uint32_t lbase = lds_addr(kst + (n * NW + wave) * 1024);
+        dma16s(kt, (uint32_t)(2 * ((int64_t)rr * krs + 8 * k_slot<D>(row, slot))), lbase);
+        dma16s(vt, (uint32_t)(2 * ((int64_t)rr * vrs + 8 * v_slot<D>(row, slot))), lbase + K_BYTES);
+      }
+    }
+  };
+  // prologue: the first NS - 1 steps (each barrier issues one more)
+  int dma_next = 0;
+  for (; dma_next < NS - 1 && dma_next < nsteps; ++dma_next) issue_step(dma_next);
+
+  // per-lane LDS byte offsets (as in attn_fwd_kernel)
+  const int k_lane = lq * RP + 16 * k_slot<D>(lq, lh);
+  const int g16 = lane >> 4, s16 = lane & 15;
+  const int v_row = 4 * (g16 >> 1) + (s16 >> 2);
+  const int v_lane = K_BYTES + v_row * RP + 16 * v_slot<D>(v_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
+
+  int step = 0;
+#pragma unroll 1
+  for (int pass = 0; pass < 2; ++pass) {
+    const int blk = pass == 0 ? blk0 : blk1;
+    if (blk < 0) break;
+    const int nt = pass == 0 ? n0 : tr1.n_pre + tr1.n2;
+    const TileRange tr = pass == 0 ? tr0 : tr1;
+
+    const int row0 = blk * BM + 32 * wave;
+    const bool valid = row0 < g.S;
+    const int i = row0 + lq;  // this lane's query row
+    bf16x8_t qf[DK];
+    {
+      const bool ok = valid && i < g.S;
+      const uint16_t* src = qh + (int64_t)(ok ? i : 0) * qrs + 8 * lh;
+#pragma unroll
+      for (int kk = 0; kk < DK; ++kk) {
+        u32x4_t val = *(const u32x4_t*)(src + 16 * kk);
+        if (!ok) val = u32x4_t{0u, 0u, 0u, 0u};
+        if constexpr (kSigFold) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            val[w] = pack_bf16x2(__uint_as_float(val[w] << 16) * kq, __uint_as_float(val[w] & 0xffff0000u) * kq);
+        }
+        qf[kk] = __builtin_bit_cast(bf16x8_t, val);
+      }
+    }
+    // this wavefront's tile classes: hull [ulo, uhi], common interval [ilo, ihi]
+    const int ra = row0, rb = imin32(row0 + 31, g.S - 1);
+    const int c_ulo = key_lo(g, ra), c_uhi = key_hi(g, rb), c_ilo = key_lo(g, rb), c_ihi = key_hi(g, ra);
+    auto key_class = [&](int c, int d) {  // keys [c, d] against this wavefront's rows
+      if (!valid) return (int)TILE_EMPTY;
+      const bool tail = d > g.S - 1;
+      if (!tail && d < g.prefix) return (int)TILE_FULL;
+      if (c_ulo > c_uhi || c > c_uhi || d < c_ulo) return c < g.prefix ? (int)TILE_PARTIAL : (int)TILE_EMPTY;
+      if (!tail && c >= c_ilo && d <= c_ihi) return (int)TILE_FULL;
+      return (int)TILE_PARTIAL;
+    };
+
+    f32x16_t oacc[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+#pragma unroll 1
+    for (int it = 0; it < nt; ++it, ++step) {
+      // wait for this step's tile (NS - 2 later steps may stay in flight), then the barrier
+      if constexpr (NS >= 3) {
+        if (dma_next - (step + 1) >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (dma_next < nsteps) issue_step(dma_next++);
+      const char* St = lds + (step % NS) * STAGE_BYTES;
+      const int jt0 = tile_at(tr, it) * BN;
+
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int jb = jt0 + 32 * kb;
+        const int cls = key_class(jb, jb + 31);
+        if (cls == TILE_EMPTY) continue;
+        const char* Kb = St + 32 * kb * RP;
+        f32x16_t s;
+        if constexpr (kBiasInit) {
+          const float b0 = bq * (float)(jb + 4 * lh - i);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s[e] = __builtin_fmaf(bq, (float)(8 * (e >> 2) + (e & 3)), b0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s[e] = 0.f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < DK; ++kk) {
+          const bf16x8_t a = *(const bf16x8_t*)(Kb + (k_lane ^ (32 * kk)));
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s, 0, 0, 0);
+        }
+        // score modifier -> t (in place)
+        if constexpr (!kScaledSoftmax && !kRawRelu && !kSigFold) {
+          const int jbase = jb + 4 * lh;
+          const float ksb = ALIBI ? ks * (float)(jbase - i) + k0 : k0;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int rc = 8 * (e >> 2) + (e & 3);
+            const float qk = s[e];
+            float lin;
+            if constexpr (ALIBI && !kBiasInit) lin = __builtin_fmaf(qk, kq, __builtin_fmaf(ks, (float)rc, ksb));
+            else if constexpr (NORM == NORM_SIGMOID && !SOFTCAP) lin = __builtin_fmaf(qk, kq, k0);
+            else lin = qk * kq;
+            if constexpr (kCapR) {
+              s[e] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(lin));
+            } else if constexpr (SOFTCAP) {
+              const float u = __builtin_amdgcn_exp2f(lin);
+              s[e] = __builtin_fmaf(__builtin_amdgcn_rcpf(1.0f + u), sc_a, sc_b);
+            } else {
+              s[e] = lin;
+            }
+          }
+        }
+        if (cls == TILE_PARTIAL) {
+          const uint32_t hidden = hidden_bits(g, i, jb + 4 * lh);
+          uint32_t hide_bits;
+          asm("s_mov_b32 %0, %1" : "=s"(hide_bits) : "i"((NORM == NORM_SIGMOID || kCapR) ? 0x7f800000 : 0xff800000));
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int rc = 8 * (e >> 2) + (e & 3);
+            uint32_t m = (uint32_t)__builtin_amdgcn_sbfe((int)hidden, rc, 1);
+            asm("" : "+v"(m));
+            s[e] = __uint_as_float((m & hide_bits) | (~m & __float_as_uint(s[e])));
+          }
+        }
+
+        // normaliser -> p, packed to bf16 pairs
+        uint32_t pk[8];
+        if constexpr (NORM == NORM_SOFTMAX) {
+          float mx = s[0];
+          if constexpr (kCapR) {
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mx = fminf(mx, s[e]);
+            mx = __builtin_fmaf(mx, sc_a, sc_b);
+          } else {
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
+          }
+          mx = xhalf_max(mx);
+          if constexpr (kScaledSoftmax) mx = mx * kq;
+          const float m_new = (mx > m_run + kRescaleLog2) ? mx : m_run;
+          if (__any(m_new != m_run)) {
+            const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) oacc[db][e] *= alpha;
+            m_run = m_new;
+          }
+          const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+          float ls = l_run;
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            float p0, p1;
+            if constexpr (kScaledSoftmax) {
+              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], kq, -m_use));
+              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], kq, -m_use));
+            } else if constexpr (kCapR) {
+              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], sc_a, sc_b - m_use));
+              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], sc_a, sc_b - m_use));
+            } else {
+              p0 = __builtin_amdgcn_exp2f(s[2 * w] - m_use);
+              p1 = __builtin_amdgcn_exp2f(s[2 * w + 1] - m_use);
+            }
+            const bf16x2_t pb = pack2(p0, p1);
+            ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);
+            pk[w] = __builtin_bit_cast(uint32_t, pb);
+          }
+          l_run = ls;
+        } else {
+#pragma unroll
+          for (int w = 0; w < 8; ++w) {
+            float p0 = s[2 * w], p1 = s[2 * w + 1];
+            if constexpr (kSigFold) {
+              p0 = __builtin_amdgcn_rcpf(__builtin_fmaf(sig_c, __builtin_amdgcn_exp2f(p0), 1.0f));
+              p1 = __builtin_amdgcn_rcpf(__builtin_fmaf(sig_c, __builtin_amdgcn_exp2f(p1), 1.0f));
+            } else if constexpr (NORM == NORM_SIGMOID) {
+              p0 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p0));
+              p1 = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(p1));
+            } else {
+              p0 = relu0(p0);
+              p1 = relu0(p1);
+            }
+            pk[w] = __builtin_bit_cast(uint32_t, pack2(p0, p1));
+          }
+        }
+
+        // O^T += V^T P^T, 16-key chunk by chunk
+        typedef short i16x8_t __attribute__((ext_vector_type(8)));
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const u32x4_t w4 = {pk[4 * half], pk[4 * half + 1], pk[4 * half + 2], pk[4 * half + 3]};
+          const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, w4);
+#pragma unroll
+          for (int db = 0; db < DB; db += 2) {
+            const char* pa = Kb + 16 * half * RP + (v_lane ^ (64 * db));  // v_lane includes K_BYTES
+            const char* pb2 = Kb + 16 * half * RP + (v_lane ^ (64 * (db + 1)));
+            const i16x4_t lo0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)pa);
+            const i16x4_t hi0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(pa + 8 * RP));
+            const i16x4_t lo1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)pb2);
+            const i16x4_t hi1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(pb2 + 8 * RP));
+            const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo0, hi0, 0, 1, 2, 3, 4, 5, 6, 7));
+            const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, (i16x8_t)__builtin_shufflevector(lo1, hi1, 0, 1, 2, 3, 4, 5, 6, 7));
+            oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, pf, oacc[db], 0, 0, 0);
+            oacc[db + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf, oacc[db + 1], 0, 0, 0);
+          }
+        }
+      }
+    }
+
+    // ---- epilogue of this block: normalise and store ---------------------------
+    float f;
+    if constexpr (NORM == NORM_SOFTMAX) {
+      const float lt = xhalf_sum(l_run);
+      f = lt > 0.f ? 1.0f / lt : 0.f;
+      if (p.lse != nullptr && lh == 0 && valid && i < g.S) {
+        const float lse2 = lt > 0.f ? m_run + __builtin_amdgcn_logf(lt) : -INFINITY;
+        p.lse[b * p.lse_sb + h * p.lse_sh + (t0 + (int64_t)g.dil * i) * p.lse_ss] = lse2 * kLn2;
+      }
+    } else {
+      f = post;
+    }
+    if (valid && i < g.S) {
+      uint16_t* dst = oh + (int64_t)i * ors + 4 * lh;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          u32x2_t w;
+          w[0] = pack_bf16x2(oacc[db][4 * gq + 0] * f, oacc[db][4 * gq + 1] * f);
+          w[1] = pack_bf16x2(oacc[db][4 * gq + 2] * f, oacc[db][4 * gq + 3] * f);
+          *(u32x2_t*)(dst + 32 * db + 8 * gq) = w;
+        }
+    }
+  }
+}
+
+}  // namespace chia

@@ -219,14 +219,16 @@ int chia_attn_fwd_fp8(const chia_attn_fp8_args* args, void* stream);
  * benchmark's FLOP accounting; the reference has no counterpart (its timer,
  * extra_bench.py:8-22, counts latency only). */
 typedef struct chia_attn_plan_info {
-  int32_t block_m;          /* query rows per workgroup (two row blocks) */
-  int32_t block_n;          /* keys per KV tile */
+  int32_t block_m;          /* query rows a workgroup computes per KV tile: two row blocks
+                               (paired core), one (head_dim 128 one-block core) */
+  int32_t block_n;          /* keys per computed step: the 64-key KV tile (paired core) or
+                               its 32-key halves (one-block core); tile counts below use it */
   int32_t wave_m;           /* rows of one computed sub-tile (32) */
   int32_t waves;            /* wavefronts per workgroup */
   int64_t workgroups;       /* grid size */
-  int64_t tiles_total;      /* (workgroup, KV tile) pairs of the dense grid */
-  int64_t tiles_visited;    /* (workgroup, KV tile) pairs loaded into LDS */
-  int64_t wave_tiles_visited; /* (32-row block, KV tile) pairs computed (wave_m x block_n) */
+  int64_t tiles_total;      /* (workgroup step, block_n keys) pairs of the dense grid */
+  int64_t tiles_visited;    /* (workgroup step, block_n keys) pairs loaded into LDS */
+  int64_t wave_tiles_visited; /* (32-row block, block_n keys) pairs computed (wave_m x block_n) */
   int64_t wave_tiles_partial; /* of which need the per-element mask */
   int64_t pairs_visible;    /* exact number of visible (i, j) pairs over B*H */
   int32_t residues;         /* dilation classes the problem splits into */

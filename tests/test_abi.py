@@ -173,6 +173,38 @@ def test_plan_geometry(lib_built):
         assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]
 
 
+def test_plan_geometry_head_dim_128(lib_built):
+    # head_dim 128 runs the one-block core: 128-row blocks, one per workgroup
+    # step, computed in 32-key steps (block_n 32); causal pairs blocks (i, n-1-i)
+    p = _lib.plan(make_args(batch=2, heads=32, seqlen=2048, head_dim=128, causal=True))
+    assert (p["waves"], p["block_m"], p["block_n"]) == (4, 128, 32)
+    assert p["workgroups"] == 2 * 32 * 8
+    # full rows: one block per workgroup
+    p = _lib.plan(make_args(batch=2, heads=32, seqlen=2048, head_dim=128, norm="sigmoid", causal=False))
+    assert (p["block_m"], p["block_n"], p["workgroups"]) == (128, 32, 2 * 32 * 16)
+    # dense full rows: every 32 x 32 step of every block is computed
+    assert p["wave_tiles_visited"] == p["tiles_total"] * 4 == 2 * 32 * (2048 // 32) * (2048 // 32)
+    # full rows of 4096+ keys without a score modifier: the paired core
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=4096, head_dim=128, norm="sigmoid", causal=False))
+    assert (p["waves"], p["block_m"], p["block_n"]) == (4, 256, 64)
+    # ... but with a softcap (or too few workgroups for two per CU) the one-block core
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=4096, head_dim=128, softcap=30.0, causal=False))
+    assert (p["block_m"], p["block_n"]) == (128, 32)
+    p = _lib.plan(make_args(batch=1, heads=4, seqlen=4096, head_dim=128, norm="relu", causal=False))
+    assert (p["block_m"], p["block_n"]) == (128, 32)
+    # every visible pair lies inside a computed 32 x block_n step, and the steps
+    # are fewer than with 64-key tiles on a band
+    for kw in (dict(causal=True), dict(causal=True, window=256), dict(causal=False, block=256),
+               dict(causal=True, dilation=2, window=1024), dict(causal=True, prefix=1024)):
+        p = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=128, **kw))
+        assert p["block_n"] == 32
+        assert p["wave_tiles_visited"] * 32 * 32 >= p["pairs_visible"]
+        assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]
+        p64 = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=64, **kw))
+        assert p["wave_tiles_visited"] * 32 <= p64["wave_tiles_visited"] * 64
+        assert p64["pairs_visible"] == p["pairs_visible"]
+
+
 def _bwd_ready_args(norm="softmax", **kw):
     """Forward args with fake (aligned, never dereferenced) device pointers."""
     a = make_args(batch=1, heads=4, seqlen=128, head_dim=64, norm=norm)
