@@ -49,9 +49,16 @@
 //   four rows x 64 bytes of one 32-lane transposed-read pass do.  With rows
 //   of a multiple of 128 bytes every fragment offset is a per-lane base XOR a
 //   compile-time constant.
-//   The softmax runs per tile in the exp2 domain with a lazily moved
-//   reference max: the running max (and the O / l rescale) only changes when
-//   a tile's max exceeds it by more than kRescaleLog2, so p <= 2^kRescaleLog2.
+//   The softmax runs per tile in the exp2 domain against a lazily moved
+//   reference max.  A tile's weights are first computed against the running
+//   reference m; only when a row has no reference yet, or a lane's partial
+//   row sum over the tile exceeds kLazyBound (some weight may exceed it), is
+//   the tile's row max computed: the reference then moves to it when it
+//   exceeds m by more than kRescaleLog2 (rescaling O and l), and the tile's
+//   weights are recomputed.  So p <= kLazyBound, and the row max -- about a
+//   quarter of the plain softmax's vector instructions per score -- is skipped
+//   on almost every tile.  ALiBi, whose bias raises the row max tile after tile, always
+//   takes the exact path.
 //   The row sum l accumulates the bf16-rounded weights the PV MFMA consumes
 //   (v_dot2c_f32_bf16 against (1, 1): one instruction per two weights).
 #pragma once
@@ -75,6 +82,7 @@ enum Norm : int { NORM_SOFTMAX = 0, NORM_SIGMOID = 1, NORM_RELU = 2 };
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
+constexpr float kLazyBound = 65536.0f;  // partial row sum of one tile that triggers an exact max
 constexpr int kBN = 64;
 
 struct FwdParams {
@@ -242,6 +250,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // the exponential's argument together with the reference max.
   constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
   constexpr bool kSigFold = NORM == NORM_SIGMOID && !ALIBI && !SOFTCAP;
+  constexpr bool kLazyMax = !ALIBI;  // softmax: the tile max only on demand
 
   constexpr bool kPipe = Pipelined<D, NW, NORM, ALIBI, SOFTCAP>::value;
   // LDS stages: 4 for 4-wavefront workgroups (up to three tiles in flight;
@@ -603,68 +612,90 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     // normaliser -> p, packed to bf16 pairs (pk[st][w] holds registers 2w, 2w+1)
     uint32_t pk[NSTR][8];
     if constexpr (NORM == NORM_SOFTMAX) {
-      // joint row max over the tile's key blocks of each query block
-      float mq[QB] = {-INFINITY, -INFINITY};
+      // Weights against the running reference max: p = 2^(t - m).  The
+      // tile's own max is only computed when a row has no reference yet or a
+      // lane's partial row sum over the tile exceeds kLazyBound: then some
+      // weight may exceed it, the reference moves to the tile's max and the
+      // tile's weights are recomputed.  Otherwise every p <= kLazyBound.
+      auto exps = [&](float* lt) __attribute__((always_inline)) {
 #pragma unroll
-      for (int st = 0; st < NSTR; ++st) {
-        float mx = sacc[st][0];
-        if constexpr (kCapR) {  // t = sc_a r + sc_b with sc_a < 0: max t <-> min r
+        for (int st = 0; st < NSTR; ++st) {
+          const int qb = qb_of(st);
+          const float m_use = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb];
+          float ls = lt[qb];
 #pragma unroll
-          for (int e = 1; e < 16; ++e) mx = fminf(mx, sacc[st][e]);
-          mx = __builtin_fmaf(mx, sc_a, sc_b);
-        } else {
-#pragma unroll
-          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+          for (int w = 0; w < 8; ++w) {
+            float p0, p1;
+            if constexpr (kScaledSoftmax) {
+              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, -m_use));
+              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, -m_use));
+            } else if constexpr (kCapR) {
+              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], sc_a, sc_b - m_use));
+              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], sc_a, sc_b - m_use));
+            } else {
+              p0 = __builtin_amdgcn_exp2f(sacc[st][2 * w] - m_use);
+              p1 = __builtin_amdgcn_exp2f(sacc[st][2 * w + 1] - m_use);
+            }
+            const bf16x2_t pb = pack2(p0, p1);
+            ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);  // row sum of the bf16 weights
+            pk[st][w] = __builtin_bit_cast(uint32_t, pb);
+          }
+          lt[qb] = ls;
         }
-        mq[qb_of(st)] = fmaxf(mq[qb_of(st)], mx);
-      }
-      float m_new[QB];
-      bool moved = false;
+      };
+      float lt[QB] = {0.f, 0.f};
+      // wavefront-uniform decision: every lane takes the same path
+      bool fresh = !kLazyMax;  // ALiBi moves the row max with every tile: always exact
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        if (WIDE && qb == 0) continue;
-        float mx = xhalf_max(mq[qb]);
-        if constexpr (kScaledSoftmax) mx = mx * kq;  // kq > 0
-        m_new[qb] = (mx > m_run[qb] + kRescaleLog2) ? mx : m_run[qb];
-        moved |= m_new[qb] != m_run[qb];
+      for (int qb = 0; qb < QB; ++qb)
+        if (!(WIDE && qb == 0)) fresh |= m_run[qb] == -INFINITY;
+      bool exact = __any(fresh);
+      if (!exact) {
+        exps(lt);
+        bool big = false;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+          if (!(WIDE && qb == 0)) big |= !(lt[qb] <= kLazyBound);
+        exact = __any(big);
       }
-      if (__any(moved)) {
+      if (exact) {
+        // joint row max over the tile's key blocks of each query block
+        float mq[QB] = {-INFINITY, -INFINITY};
+#pragma unroll
+        for (int st = 0; st < NSTR; ++st) {
+          float mx = sacc[st][0];
+          if constexpr (kCapR) {  // t = sc_a r + sc_b with sc_a < 0: max t <-> min r
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mx = fminf(mx, sacc[st][e]);
+            mx = __builtin_fmaf(mx, sc_a, sc_b);
+          } else {
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+          }
+          mq[qb_of(st)] = fmaxf(mq[qb_of(st)], mx);
+        }
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           if (WIDE && qb == 0) continue;
-          const float alpha = (m_run[qb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new[qb]);
-          l_run[qb] *= alpha;
+          float mx = xhalf_max(mq[qb]);
+          if constexpr (kScaledSoftmax) mx = mx * kq;  // kq > 0
+          const float m_new = (mx > m_run[qb] + kRescaleLog2) ? mx : m_run[qb];
+          if (m_new != m_run[qb]) {  // per lane: the row's O and l follow its reference
+            const float alpha = (m_run[qb] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+            l_run[qb] *= alpha;
 #pragma unroll
-          for (int db = 0; db < DB; ++db)
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) oacc[db][qb][e] *= alpha;
-          m_run[qb] = m_new[qb];
-        }
-      }
-#pragma unroll
-      for (int st = 0; st < NSTR; ++st) {
-        const int qb = qb_of(st);
-        const float m_use = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb];
-        float ls = l_run[qb];
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          float p0, p1;
-          if constexpr (kScaledSoftmax) {
-            p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, -m_use));
-            p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, -m_use));
-          } else if constexpr (kCapR) {
-            p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], sc_a, sc_b - m_use));
-            p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], sc_a, sc_b - m_use));
-          } else {
-            p0 = __builtin_amdgcn_exp2f(sacc[st][2 * w] - m_use);
-            p1 = __builtin_amdgcn_exp2f(sacc[st][2 * w + 1] - m_use);
+              for (int e = 0; e < 16; ++e) oacc[db][qb][e] *= alpha;
+            m_run[qb] = m_new;
           }
-          const bf16x2_t pb = pack2(p0, p1);
-          ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);  // row sum of the bf16 weights
-          pk[st][w] = __builtin_bit_cast(uint32_t, pb);
+          lt[qb] = 0.f;
         }
-        l_run[qb] = ls;
+        exps(lt);
       }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+        if (!(WIDE && qb == 0)) l_run[qb] += lt[qb];
     } else {
 #pragma unroll
       for (int st = 0; st < NSTR; ++st) {
