@@ -46,11 +46,13 @@ def kernel_name(op: str, B: int, H: int, S: int, D: int, params: dict) -> str:
     from chia_proj_amd.accounting import core_plan_kwargs
 
     kw = core_plan_kwargs(op, H, params)
-    waves = plan(batch=B, heads=H, seqlen=S, head_dim=D, **kw)["waves"]
+    p = plan(batch=B, heads=H, seqlen=S, head_dim=D, **kw)
     norm = {"softmax": 0, "sigmoid": 1, "relu": 2}[kw.get("norm", "softmax")]
     al = "true" if kw["alibi"] else "false"
     sc = "true" if kw.get("softcap", 0) else "false"
-    return f"void chia::attn_fwd_kernel<{D}, {waves}, {norm}, {al}, {sc}>(chia::FwdParams)"
+    if p["block_n"] == 32:  # the head_dim 128 one-block core
+        return f"void chia::attn_fwd_q1_kernel<{D}, {norm}, {al}, {sc}>(chia::FwdParams)"
+    return f"void chia::attn_fwd_kernel<{D}, {p['waves']}, {norm}, {al}, {sc}>(chia::FwdParams)"
 
 
 def load_traffic(suite: str, op: str, kname: str):
@@ -239,6 +241,8 @@ def reference_report(dev, args) -> int:
     import glob
     import importlib.util
 
+    import torch
+
     from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, rates
     from chia_proj_amd.timing import CacheFlusher, cold_us, median_us
     from chia_proj_amd.workloads import draw_inputs, reference_suite
@@ -256,6 +260,14 @@ def reference_report(dev, args) -> int:
     cases = reference_suite()
     q, k, v, _ = draw_inputs(cases[0], dev)
     flusher = CacheFlusher(device=dev)
+    if args.pmc_mode:  # for rocprofv3 --pmc: each variant twice after a cache flush, nothing timed
+        for c in cases:
+            for _ in range(2):
+                flusher()
+                loaded[c.op](q, k, v)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_mode": True, "suite": "reference", "variants": [c.op for c in cases]}), flush=True)
+        return 0
     rows, tot_us, tot_flops = {}, 0.0, 0.0
     for c in cases:
         fn = lambda f=loaded[c.op]: f(q, k, v)  # noqa: E731
