@@ -134,16 +134,18 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
 
 // The forward's core and geometry.  Head dim 64: the paired core.  Head dim
 // 128: the one-block core (two wavefronts per SIMD), except on full rows
-// (no causal pairing, window or block) of 4096 keys or more without a score
+// (no causal pairing, window or block) of 2048 keys or more without a score
 // modifier and with two 4-wavefront workgroups per CU, where the paired
 // core's pipelined run and its K/V tiles shared by two row blocks measured
-// faster (B4 H16 S4096: sigmoid 504 vs 533 us, ReLU 447 vs 465 us).
+// faster (B4 H16 D128, sigmoid / ReLU: 141.8 / 122.9 us against 155.9 / 129.0
+// at S2048, 504 / 447 against 533 / 465 at S4096; at S1024 the one-block
+// core wins, 45.5 against 61.1 us for sigmoid).
 Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const ScorePath& sp) {
   Geometry geo = paired_geometry(m, a->batch, a->heads);
   if (a->head_dim != 128) return geo;
   const bool banded = m.hi < kInf || m.blk > 0;
   const int32_t s0 = residue_geom(m, 0).S;
-  if (!geo.zigzag && !banded && s0 >= 4096 && !sp.alibi && !sp.softcap && geo.waves == 4) return geo;
+  if (!geo.zigzag && !banded && s0 >= 2048 && !sp.alibi && !sp.softcap && geo.waves == 4) return geo;
   geo.q1 = true;
   geo.waves = 4;
   geo.rows = 128;

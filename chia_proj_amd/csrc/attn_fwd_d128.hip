@@ -1,5 +1,5 @@
 // attn_fwd_d128.hip -- instantiations of the paired forward core for head_dim
-// 128.  The dispatcher runs it only on full rows of 4096 keys or more without
+// 128.  The dispatcher runs it only on full rows of 2048 keys or more without
 // a score modifier, with 4 wavefronts per workgroup (every other head_dim
 // 128 forward runs the one-block core, attn_fwd_q1_d128.hip): the three
 // normalisers.

@@ -11,8 +11,9 @@
 // wavefront's MFMAs.  One query block per wavefront needs ~180 VGPRs (no
 // spills), two wavefronts fit on each SIMD, and the SIMD interleaves them.
 // The paired core keeps the case where it measured faster: full rows
-// (no causal pairing, window or block) of 4096 keys or more, where sharing
-// each K/V tile between two row blocks halves the K/V reads.
+// (no causal pairing, window or block) of 2048 keys or more without a score
+// modifier, where sharing each K/V tile between two row blocks halves the
+// K/V reads.
 //
 // Work decomposition
 //   * a workgroup of 4 wavefronts owns row blocks of 128 rows of one (batch,
