@@ -22,7 +22,7 @@ LIB_NAME = "libchia_attn.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 BUILD_DIR = REPO_DIR / "_build"
 
-SOURCES = ["attn_fwd_d64.hip", "attn_fwd_d128.hip", "attn_fwd_q1_d128.hip", "attn_bwd_d64.hip", "attn_bwd_d128.hip", "attn_fp8.hip", "attn_api.hip"]
+SOURCES = ["attn_fwd_d64.hip", "attn_fwd_d128.hip", "attn_fwd_q1_d64.hip", "attn_fwd_q1_d128.hip", "attn_bwd_d64.hip", "attn_bwd_d128.hip", "attn_fp8.hip", "attn_api.hip"]
 HEADERS = ["attn_fwd_kernel.h", "attn_fwd_q1_kernel.h", "lds_layout.h", "mask.h"]
 
 ARCH = "gfx950"

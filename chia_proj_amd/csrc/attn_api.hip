@@ -19,6 +19,7 @@ namespace chia {
 
 using KernelFn = void (*)(FwdParams);
 KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
+KernelFn select_q1_kernel_d64(int norm, bool alibi, bool softcap);
 KernelFn select_kernel_d128(int norm);
 KernelFn select_q1_kernel_d128(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
@@ -104,7 +105,7 @@ struct Geometry {
                    // for the one-block core without pairing, row blocks
   int residues;
   int zigzag;
-  bool q1;         // the head_dim 128 one-block core (attn_fwd_q1_kernel.h)
+  bool q1;         // the one-block core (attn_fwd_q1_kernel.h)
   int64_t workgroups;
 };
 
@@ -132,7 +133,10 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
   return geo;
 }
 
-// The forward's core and geometry.  Head dim 64: the paired core.  Head dim
+// The forward's core and geometry.  Head dim 64: the paired core, or for a
+// window or block mask the one-block core at four wavefronts per SIMD (north
+// star: local 53.2 -> 42.6 us, sliding window 53.1 -> 42.9, block-diagonal
+// 39.0 -> 30.5, dilated 61.6 -> 57.5; cold-cache 12-20 % less).  Head dim
 // 128: the one-block core (two wavefronts per SIMD), except on full rows
 // (no causal pairing, window or block) of 2048 keys or more without a score
 // modifier and with two 4-wavefront workgroups per CU, where the paired
@@ -142,10 +146,11 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
 // core wins, 45.5 against 61.1 us for sigmoid).
 Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const ScorePath& sp) {
   Geometry geo = paired_geometry(m, a->batch, a->heads);
-  if (a->head_dim != 128) return geo;
   const bool banded = m.hi < kInf || m.blk > 0;
   const int32_t s0 = residue_geom(m, 0).S;
-  if (!geo.zigzag && !banded && s0 >= 2048 && !sp.alibi && !sp.softcap && geo.waves == 4) return geo;
+  if (a->head_dim == 64 && !banded) return geo;
+  if (a->head_dim == 128 && !geo.zigzag && !banded && s0 >= 2048 && !sp.alibi && !sp.softcap && geo.waves == 4)
+    return geo;
   geo.q1 = true;
   geo.waves = 4;
   geo.rows = 128;
@@ -230,7 +235,8 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   p.post_scale = a->post_scale;
   p.lse = a->norm == CHIA_ATTN_NORM_SOFTMAX ? lse : nullptr;
 
-  KernelFn fn = a->head_dim == 64 ? select_kernel_d64(waves, (int)a->norm, sp.alibi, sp.softcap)
+  KernelFn fn = a->head_dim == 64 ? (geo.q1 ? select_q1_kernel_d64((int)a->norm, sp.alibi, sp.softcap)
+                                            : select_kernel_d64(waves, (int)a->norm, sp.alibi, sp.softcap))
                : geo.q1            ? select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap)
                                    : select_kernel_d128((int)a->norm);
   void* kargs[] = {&p};

@@ -1,6 +1,6 @@
 // attn_fwd_q1_d128.hip -- instantiations of the one-query-block-per-wavefront
 // forward core (attn_fwd_q1_kernel.h) for head_dim 128: 3 normalisers x
-// ALiBi on/off x softcap on/off.
+// ALiBi on/off x softcap on/off (attn_fwd_q1_d64.hip: head_dim 64).
 #include "attn_fwd_q1_kernel.h"
 
 namespace chia {

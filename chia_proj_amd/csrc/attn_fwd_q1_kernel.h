@@ -1,19 +1,23 @@
-// attn_fwd_q1_kernel.h -- the head_dim 128 forward core: one 32-row query
-// block per wavefront, two wavefronts per SIMD.
+// attn_fwd_q1_kernel.h -- the one-block forward core: one 32-row query block
+// per wavefront.  It runs every head_dim 128 forward but long full rows, and
+// the banded masks (window, block) at head_dim 64.
 //
 // Reference semantics: the eager closures of extra_bench.py:32-62 and
 // sigmoid_fix.py:34-40, as for attn_fwd_kernel.h, whose helpers (DMA, LDS
 // layout, score constants, masks, packing) this kernel shares.
 //
-// Why a second core: at head_dim 128 the paired core (two query blocks per
-// wavefront) holds 128 accumulator registers of O alone and runs one
-// wavefront per SIMD, so nothing hides its softmax behind another
-// wavefront's MFMAs.  One query block per wavefront needs ~180 VGPRs (no
-// spills), two wavefronts fit on each SIMD, and the SIMD interleaves them.
-// The paired core keeps the case where it measured faster: full rows
-// (no causal pairing, window or block) of 2048 keys or more without a score
-// modifier, where sharing each K/V tile between two row blocks halves the
-// K/V reads.
+// Why a second core.
+//   * head_dim 128: the paired core (two query blocks per wavefront) holds 128
+//     accumulator registers of O alone and runs one wavefront per SIMD, so
+//     nothing hides its softmax behind another wavefront's MFMAs.  One query
+//     block per wavefront needs ~180 VGPRs (no spills), two wavefronts fit on
+//     each SIMD, and the SIMD interleaves them.  The paired core keeps the
+//     case where it measured faster: full rows (no causal pairing, window or
+//     block) of 2048 keys or more without a score modifier, where sharing each
+//     K/V tile between two row blocks halves the K/V reads.
+//   * head_dim 64, banded masks: a workgroup's key range is its rows plus the
+//     window, a few tiles; four wavefronts per SIMD (~110 VGPRs) hide the
+//     latency of those few tiles better than the paired core's two.
 //
 // Work decomposition
 //   * a workgroup of 4 wavefronts owns row blocks of 128 rows of one (batch,
@@ -25,23 +29,24 @@
 //   * the K / V tiles (64 keys) of the block's key range go HBM -> LDS with
 //     global_load_lds_dwordx4 through NS stages (one barrier per tile); the
 //     DMA runs across the boundary between the two blocks of a pair;
-//   * a tile is computed as two 32-key steps: S^T = K Q^T (8 MFMAs), score
-//     modifier, mask on partial steps, normaliser with its own row-max
-//     update, then O^T += V^T P^T (8 MFMAs), with the matrix-core layouts of
-//     the paired core (lane = query column; V^T read with
-//     ds_read_b64_tr_b16); a 32-key step no row of the wavefront sees is
+//   * a tile is computed as two 32-key steps: S^T = K Q^T (D / 16 MFMAs),
+//     score modifier, mask on partial steps, normaliser with its own row-max
+//     update, then O^T += V^T P^T (D / 16 MFMAs), with the matrix-core layouts
+//     of the paired core (lane = query column; V^T read with
+//     ds_read_b64_tr_b16); a 32-key step that no row of the wavefront sees is
 //     skipped.
 #pragma once
 #include "attn_fwd_kernel.h"
 
 namespace chia {
 
-// Waves per SIMD the register budget targets, and LDS stages per workgroup
-// (two workgroups per CU x 2 stages x 32 KB at head_dim 128).
+// Waves per SIMD the register budget targets, and LDS stages per workgroup:
+// head_dim 64, four workgroups per CU x 2 stages x 16 KB; head_dim 128, two
+// workgroups per CU x 2 stages x 32 KB.
 template <int D>
 struct Q1Config {
-  static_assert(D == 128, "the one-block core is built for head_dim 128");
-  static constexpr int occupancy = 2;
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static constexpr int occupancy = D == 64 ? 4 : 2;
   static constexpr int stages = 2;
 };
 

@@ -32,6 +32,7 @@ struct BwdKernels {
   BwdKernelFn stats, dq, dkdv;
 };
 KernelFn select_kernel_d64(int, int, bool, bool) { return nullptr; }
+KernelFn select_q1_kernel_d64(int, bool, bool) { return nullptr; }
 KernelFn select_kernel_d128(int) { return nullptr; }
 KernelFn select_q1_kernel_d128(int, bool, bool) { return nullptr; }
 BwdKernels select_bwd_kernels_d64(int, bool, bool) { return BwdKernels{nullptr, nullptr, nullptr}; }

@@ -162,14 +162,17 @@ def test_plan_geometry(lib_built):
     # causal without a window pairs row blocks (i, n-1-i); every pair is one workgroup
     p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, causal=True))
     assert p["waves"] == 4 and p["block_m"] == 256 and p["workgroups"] == 4 * 16 * 8
-    # a window keeps 2-wavefront workgroups
-    p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, causal=True, window=256))
-    assert p["waves"] == 2 and p["block_m"] == 128
-    # every visible pair is inside a computed 32 x 64 sub-tile
+    # a window or block mask runs the one-block core: 128-row blocks, one per
+    # workgroup, 32-key steps
+    for kw in (dict(causal=True, window=256), dict(causal=False, block=256), dict(causal=True, window=129)):
+        p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, **kw))
+        assert (p["waves"], p["block_m"], p["block_n"], p["workgroups"]) == (4, 128, 32, 4 * 16 * 16)
+    # every visible pair is inside a computed 32 x block_n step
     for kw in (dict(causal=True), dict(causal=True, window=256), dict(causal=False, block=256),
                dict(causal=True, dilation=2, window=1024), dict(causal=True, prefix=1024)):
         p = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=64, **kw))
-        assert p["wave_tiles_visited"] * 32 * 64 >= p["pairs_visible"]
+        assert p["block_n"] == (32 if ("window" in kw or "block" in kw) else 64)
+        assert p["wave_tiles_visited"] * 32 * p["block_n"] >= p["pairs_visible"]
         assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]
 
 
@@ -202,7 +205,7 @@ def test_plan_geometry_head_dim_128(lib_built):
         assert p["wave_tiles_visited"] * 32 * 32 >= p["pairs_visible"]
         assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]
         p64 = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=64, **kw))
-        assert p["wave_tiles_visited"] * 32 <= p64["wave_tiles_visited"] * 64
+        assert p["wave_tiles_visited"] * 32 <= p64["wave_tiles_visited"] * p64["block_n"]
         assert p64["pairs_visible"] == p["pairs_visible"]
 
 
