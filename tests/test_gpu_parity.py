@@ -149,6 +149,51 @@ def test_edge_cases(name, S, D, kw):
     assert res.ok, f"{name}: {res.status} {res.stats}"
 
 
+RISING = [
+    ("causal", dict(causal=True)),
+    ("prefix256", dict(causal=True, prefix=256)),
+    ("full", dict(causal=False)),
+    ("softcap50", dict(causal=True, softcap=50.0)),
+    ("headscale", dict(causal=True, head_scale="per-head")),
+]
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 512), (4, 16, 2048)], ids=["B1H2S512", "B4H16S2048"])
+@pytest.mark.parametrize("name,kw", RISING, ids=[r[0] for r in RISING])
+def test_softmax_rising_scores(name, kw, shape):
+    """Scores that rise along the keys: q ~ 4 u, k_j ~ (j / 2) u (u a unit vector) plus noise,
+    so a row's max climbs ~23 log2-units per 64-key tile.  The softmax weights are first
+    computed against the running reference max and, when a partial row sum over a tile exceeds
+    2^16, recomputed against the tile's max; these inputs take that path on almost every tile.
+    The smaller shape runs 2-wavefront workgroups, the larger 4-wavefront ones (PAIR, WIDE and
+    WIDE2 steps)."""
+    B, H, S = shape
+    D = 64
+    _say(f"[parity] rising scores {name} {shape}")
+    g = torch.Generator("cpu").manual_seed(S + len(name))
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    ramp = torch.arange(S, dtype=torch.float32) * 0.5
+    k = (ramp[:, None] * u + 0.3 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
+    q = (4.0 * u + 0.3 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
+    v = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    kw = dict(kw)
+    if kw.get("head_scale") == "per-head":
+        kw["head_scale"] = [0.5 + 0.1 * h for h in range(H)]
+    o = attention(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o).all()), f"{name}: non-finite output"
+    oc = o.float().cpu()
+    heads = [(0, 0), (B - 1, H - 1), (B // 2, H // 2)]
+    for b, h in heads:
+        kwh = dict(kw)
+        if "head_scale" in kwh:
+            kwh["head_scale"] = [kw["head_scale"][h]]
+        r = oracle.attention_ref(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], **kwh)
+        res = gate.north_star_gate(r[0, 0], oc[b, h])
+        assert res.ok, f"{name} b={b} h={h}: {res.status} {res.stats}"
+
+
 def test_strided_layout_and_out_param():
     """[B, S, H, D] storage viewed as [B, H, S, D] (non-contiguous) and a caller-provided out."""
     _say("[parity] strided layout")
