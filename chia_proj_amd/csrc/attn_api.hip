@@ -137,19 +137,23 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
 // window or block mask the one-block core at four wavefronts per SIMD (north
 // star: local 53.2 -> 42.6 us, sliding window 53.1 -> 42.9, block-diagonal
 // 39.0 -> 30.5, dilated 61.6 -> 57.5; cold-cache 12-20 % less).  Head dim
-// 128: the one-block core (two wavefronts per SIMD), except on full rows
-// (no causal pairing, window or block) of 2048 keys or more without a score
-// modifier and with two 4-wavefront workgroups per CU, where the paired
-// core's pipelined run and its K/V tiles shared by two row blocks measured
-// faster (B4 H16 D128, sigmoid / ReLU: 141.8 / 122.9 us against 155.9 / 129.0
-// at S2048, 504 / 447 against 533 / 465 at S4096; at S1024 the one-block
-// core wins, 45.5 against 61.1 us for sigmoid).
+// 128: the one-block core (two wavefronts per SIMD), except for sigmoid and
+// ReLU on full rows (no causal pairing, window or block) of 2048 keys or more
+// without a score modifier and with two 4-wavefront workgroups per CU, where
+// the paired core's pipelined run and its K/V tiles shared by two row blocks
+// measured faster (B4 H16 D128, sigmoid / ReLU: 141.8 / 122.9 us against
+// 155.9 / 129.0 at S2048, 504 / 447 against 533 / 465 at S4096; at S1024 the
+// one-block core wins, 45.5 against 61.1 us for sigmoid).  Softmax on such
+// rows runs the one-block core: the paired softmax kernel at head_dim 128
+// spills (17 VGPRs at one wavefront per SIMD), and the one-block core
+// measured 288.8 against 294.7 us (B4 H16 S4096, temperature).
 Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const ScorePath& sp) {
   Geometry geo = paired_geometry(m, a->batch, a->heads);
   const bool banded = m.hi < kInf || m.blk > 0;
   const int32_t s0 = residue_geom(m, 0).S;
   if (a->head_dim == 64 && !banded) return geo;
-  if (a->head_dim == 128 && !geo.zigzag && !banded && s0 >= 2048 && !sp.alibi && !sp.softcap && geo.waves == 4)
+  if (a->head_dim == 128 && a->norm != CHIA_ATTN_NORM_SOFTMAX && !geo.zigzag && !banded && s0 >= 2048 && !sp.alibi &&
+      !sp.softcap && geo.waves == 4)
     return geo;
   geo.q1 = true;
   geo.waves = 4;
@@ -239,6 +243,7 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
                                             : select_kernel_d64(waves, (int)a->norm, sp.alibi, sp.softcap))
                : geo.q1            ? select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap)
                                    : select_kernel_d128((int)a->norm);
+  if (fn == nullptr) return CHIA_ATTN_ERR_NORM;  // no instantiation for this core and normaliser
   void* kargs[] = {&p};
   hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(64 * waves), kargs,
                                    0, (hipStream_t)stream);

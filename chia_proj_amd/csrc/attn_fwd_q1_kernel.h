@@ -1,6 +1,6 @@
 // attn_fwd_q1_kernel.h -- the one-block forward core: one 32-row query block
-// per wavefront.  It runs every head_dim 128 forward but long full rows, and
-// the banded masks (window, block) at head_dim 64.
+// per wavefront.  It runs every head_dim 128 forward but long full rows of
+// sigmoid / ReLU, and the banded masks (window, block) at head_dim 64.
 //
 // Reference semantics: the eager closures of extra_bench.py:32-62 and
 // sigmoid_fix.py:34-40, as for attn_fwd_kernel.h, whose helpers (DMA, LDS
@@ -12,9 +12,10 @@
 //     nothing hides its softmax behind another wavefront's MFMAs.  One query
 //     block per wavefront needs ~180 VGPRs (no spills), two wavefronts fit on
 //     each SIMD, and the SIMD interleaves them.  The paired core keeps the
-//     case where it measured faster: full rows (no causal pairing, window or
-//     block) of 2048 keys or more without a score modifier, where sharing each
-//     K/V tile between two row blocks halves the K/V reads.
+//     case where it measured faster: sigmoid and ReLU on full rows (no causal
+//     pairing, window or block) of 2048 keys or more without a score
+//     modifier, where sharing each K/V tile between two row blocks halves the
+//     K/V reads.
 //   * head_dim 64, banded masks: a workgroup's key range is its rows plus the
 //     window, a few tiles; four wavefronts per SIMD (~110 VGPRs) hide the
 //     latency of those few tiles better than the paired core's two.
@@ -201,6 +202,11 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
   const int v_row = 4 * (g16 >> 1) + (s16 >> 2);
   const int v_lane = K_BYTES + v_row * RP + 16 * v_slot<D>(v_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
 
+  // softmax normaliser: a step's K fragments are read before its QK^T chain,
+  // and both MFMA chains issue at raised wave priority, so the SIMD's other
+  // wavefront runs its exponentials beside them (sigmoid and ReLU measured
+  // slower with either)
+  constexpr bool kPrio = NORM == NORM_SOFTMAX;
   int step = 0;
 #pragma unroll 1
   for (int pass = 0; pass < 2; ++pass) {
@@ -277,10 +283,22 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
 #pragma unroll
           for (int e = 0; e < 16; ++e) s[e] = 0.f;
         }
+        if constexpr (kPrio) {
+          __builtin_amdgcn_s_setprio(1);
+          bf16x8_t kf[DK];
 #pragma unroll
-        for (int kk = 0; kk < DK; ++kk) {
-          const bf16x8_t a = *(const bf16x8_t*)(Kb + (k_lane ^ (32 * kk)));
-          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s, 0, 0, 0);
+          for (int kk = 0; kk < DK; ++kk) kf[kk] = *(const bf16x8_t*)(Kb + (k_lane ^ (32 * kk)));
+#pragma unroll
+          for (int kk = 0; kk < DK; ++kk) s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s, 0, 0, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, DK, 0);  // the DK LDS reads first,
+          __builtin_amdgcn_sched_group_barrier(0x008, DK, 0);  // then the DK MFMAs
+          __builtin_amdgcn_s_setprio(0);
+        } else {
+#pragma unroll
+          for (int kk = 0; kk < DK; ++kk) {
+            const bf16x8_t a = *(const bf16x8_t*)(Kb + (k_lane ^ (32 * kk)));
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s, 0, 0, 0);
+          }
         }
         // score modifier -> t (in place)
         if constexpr (!kScaledSoftmax && !kRawRelu && !kSigFold) {
@@ -380,6 +398,7 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
         }
 
         // O^T += V^T P^T, 16-key chunk by chunk
+        if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
         typedef short i16x8_t __attribute__((ext_vector_type(8)));
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -399,6 +418,7 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
             oacc[db + 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, pf, oacc[db + 1], 0, 0, 0);
           }
         }
+        if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
       }
     }
 

@@ -187,10 +187,14 @@ def test_plan_geometry_head_dim_128(lib_built):
     assert (p["block_m"], p["block_n"], p["workgroups"]) == (128, 32, 4 * 16 * 8)
     # dense full rows: every 32 x 32 step of every block is computed
     assert p["wave_tiles_visited"] == p["tiles_total"] * 4 == 4 * 16 * (1024 // 32) * (1024 // 32)
-    # full rows of 2048+ keys without a score modifier: the paired core
+    # sigmoid / ReLU on full rows of 2048+ keys without a score modifier: the paired core
     for S in (2048, 4096):
-        p = _lib.plan(make_args(batch=4, heads=16, seqlen=S, head_dim=128, norm="sigmoid", causal=False))
-        assert (p["waves"], p["block_m"], p["block_n"]) == (4, 256, 64)
+        for norm in ("sigmoid", "relu"):
+            p = _lib.plan(make_args(batch=4, heads=16, seqlen=S, head_dim=128, norm=norm, causal=False))
+            assert (p["waves"], p["block_m"], p["block_n"]) == (4, 256, 64)
+        # softmax there runs the one-block core (no paired softmax kernel at head_dim 128)
+        p = _lib.plan(make_args(batch=4, heads=16, seqlen=S, head_dim=128, norm="softmax", causal=False))
+        assert (p["waves"], p["block_m"], p["block_n"]) == (4, 128, 32)
     # ... but with a softcap (or too few workgroups for two per CU) the one-block core
     p = _lib.plan(make_args(batch=4, heads=16, seqlen=4096, head_dim=128, softcap=30.0, causal=False))
     assert (p["block_m"], p["block_n"]) == (128, 32)
