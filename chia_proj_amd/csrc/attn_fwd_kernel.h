@@ -57,8 +57,10 @@
 //   exceeds m by more than kRescaleLog2 (rescaling O and l), and the tile's
 //   weights are recomputed.  So p <= kLazyBound, and the row max -- about a
 //   quarter of the plain softmax's vector instructions per score -- is skipped
-//   on almost every tile.  ALiBi, whose bias raises the row max tile after tile, always
-//   takes the exact path.
+//   on almost every tile.  ALiBi's bias grows with the key index, so its
+//   kernels walk the key tiles from the last to the first: a row's first tile
+//   then sets the reference, and the later tiles, lower by the slope times
+//   their distance, stay under it.
 //   The row sum l accumulates the bf16-rounded weights the PV MFMA consumes
 //   (v_dot2c_f32_bf16 against (1, 1): one instruction per two weights).
 #pragma once
@@ -250,7 +252,11 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // the exponential's argument together with the reference max.
   constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
   constexpr bool kSigFold = NORM == NORM_SIGMOID && !ALIBI && !SOFTCAP;
-  constexpr bool kLazyMax = !ALIBI;  // softmax: the tile max only on demand
+  // ALiBi softmax walks its key tiles from the last to the first: the bias
+  // grows with the key index, so a row's first tile fixes its max and the
+  // later ones stay under it, as the tile max only on demand needs.
+  constexpr bool kRev = ALIBI && NORM == NORM_SOFTMAX;
+  constexpr bool kLazyMax = !ALIBI || kRev;  // softmax: the tile max only on demand
 
   constexpr bool kPipe = Pipelined<D, NW, NORM, ALIBI, SOFTCAP>::value;
   // LDS stages: 4 for 4-wavefront workgroups (up to three tiles in flight;
@@ -373,6 +379,9 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // ---- KV tiles this workgroup visits ---------------------------------------
   const TileRange tr = tile_range(g, blk0 * BMH, imin32((blk1 >= 0 ? blk1 : blk0) * BMH + BMH - 1, g.S - 1), BN);
   const int ntiles = tr.n_pre + tr.n2;
+  // the tile of step k, and whether it lies in the band (not the prefix)
+  auto seq_tile = [&](int k) __attribute__((always_inline)) { return tile_at(tr, kRev ? ntiles - 1 - k : k); };
+  auto in_band = [&](int k) __attribute__((always_inline)) { return kRev ? k < tr.n2 : k >= tr.n_pre; };
 
   // Global -> LDS DMA.  Load n of wavefront w fills LDS chunks
   // [(n NW + w) 64, +64) of the K (or V) tile: lane l moves the 16-byte chunk
@@ -441,7 +450,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
 #pragma unroll
     for (int k = 0; k < kIssue; ++k)
       if (dma_next <= last) {
-        issue_tile(tile_at(tr, dma_next) * BN, dma_next & (NS - 1));
+        issue_tile(seq_tile(dma_next) * BN, dma_next & (NS - 1));
         ++dma_next;
       }
   };
@@ -457,7 +466,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   auto sync_tile = [&](int it) __attribute__((always_inline)) { sync_step(it, 1, kPipe ? it - 1 : it); };
   // prologue: the first kFly + 1 tiles (the first sync issues the next one),
   // issued before the per-block set-up below so the loads overlap it
-  for (int t = 0; t <= kFly && t < ntiles; ++t) issue_tile(tile_at(tr, t) * BN, t);
+  for (int t = 0; t <= kFly && t < ntiles; ++t) issue_tile(seq_tile(t) * BN, t);
   dma_next = imin32(kFly + 1, ntiles);
 
   // Tile classes: each query block's key hull [ulo, uhi] and common interval
@@ -645,7 +654,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       };
       float lt[QB] = {0.f, 0.f};
       // wavefront-uniform decision: every lane takes the same path
-      bool fresh = !kLazyMax;  // ALiBi moves the row max with every tile: always exact
+      bool fresh = !kLazyMax;  // the exact path: always without the lazy max, else for rows without a reference
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
         if (!(WIDE && qb == 0)) fresh |= m_run[qb] == -INFINITY;
@@ -920,7 +929,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     f32x16_t sb[2][2];
     sync_tile(ia);
     const char* S0 = lds + (ia & (NS - 1)) * STAGE_BYTES;
-    const int j0 = tile_at(tr, ia) * BN;
+    const int j0 = seq_tile(ia) * BN;
     {
       float mx[2];
       p_qk(S0, 0, sb[0]);
@@ -932,7 +941,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     for (int it = ia + 1; it < ib; ++it) {
       sync_tile(it);
       const char* St = lds + (it & (NS - 1)) * STAGE_BYTES;
-      const int jt0 = tile_at(tr, it) * BN;
+      const int jt0 = seq_tile(it) * BN;
       p_body(sb, IntTag<1>{}, Sp, 1, St, jt0, 0);
       p_body(sb, IntTag<0>{}, St, 0, St, jt0, 1);
       Sp = St;
@@ -959,12 +968,21 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
         continue;
       }
     }
-    const int jt0 = tile_at(tr, it) * BN;
+    const int jt0 = seq_tile(it) * BN;
     // Two consecutive tiles that only block 1 sees, both in full: one WIDE2
     // step behind one barrier.
     if constexpr (kWide2) {
       const int t = jt0 / BN;
-      if (it >= tr.n_pre && it + 1 < ntiles && t >= w2.lo && t + 1 <= w2.hi) {
+      if constexpr (kRev) {  // tiles t, t - 1
+        if (in_band(it) && in_band(it + 1) && t - 1 >= w2.lo && t <= w2.hi) {
+          sync_step(it, 2, it);
+          const bool none[QB] = {false, false};
+          tile_step(lds + ((it + 1) & (NS - 1)) * STAGE_BYTES, lds + (it & (NS - 1)) * STAGE_BYTES, jt0 - BN, none,
+                    IntTag<2>{});
+          ++it;
+          continue;
+        }
+      } else if (it >= tr.n_pre && it + 1 < ntiles && t >= w2.lo && t + 1 <= w2.hi) {
         sync_step(it, 2, it);
         const bool none[QB] = {false, false};
         tile_step(lds + (it & (NS - 1)) * STAGE_BYTES, lds + ((it + 1) & (NS - 1)) * STAGE_BYTES, jt0, none, IntTag<2>{});
@@ -977,9 +995,9 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     int act = 0;
     bool masked[QB] = {false, false};
     const int t = jt0 / BN;
-    if (it >= tr.n_pre && t >= fr.pf_lo && t <= fr.pf_hi) {
+    if (in_band(it) && t >= fr.pf_lo && t <= fr.pf_hi) {
       act = 3;
-    } else if (it >= tr.n_pre && t >= fr.wf_lo && t <= fr.wf_hi) {
+    } else if (in_band(it) && t >= fr.wf_lo && t <= fr.wf_hi) {
       act = 2;
     } else {
 #pragma unroll

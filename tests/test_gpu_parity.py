@@ -155,27 +155,64 @@ RISING = [
     ("full", dict(causal=False)),
     ("softcap50", dict(causal=True, softcap=50.0)),
     ("headscale", dict(causal=True, head_scale="per-head")),
+    ("window256", dict(causal=True, window=256)),
+    ("block256", dict(causal=False, block=256)),
 ]
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 512), (4, 16, 2048)], ids=["B1H2S512", "B4H16S2048"])
-@pytest.mark.parametrize("name,kw", RISING, ids=[r[0] for r in RISING])
-def test_softmax_rising_scores(name, kw, shape):
-    """Scores that rise along the keys: q ~ 4 u, k_j ~ (j / 2) u (u a unit vector) plus noise,
-    so a row's max climbs ~23 log2-units per 64-key tile.  The softmax weights are first
-    computed against the running reference max and, when a partial row sum over a tile exceeds
-    2^16, recomputed against the tile's max; these inputs take that path on almost every tile.
+ALIBI_ORDER = [
+    ("causal", dict(causal=True), 1.0),
+    ("full", dict(causal=False), 1.0),
+    ("prefix300", dict(causal=True, prefix=300), 1.0),
+    ("causal_negative", dict(causal=True), -1.0),
+    ("full_negative", dict(causal=False), -1.0),
+]
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 700), (4, 16, 2048)], ids=["B1H2S700", "B4H16S2048"])
+@pytest.mark.parametrize("name,kw,sign", ALIBI_ORDER, ids=[a[0] for a in ALIBI_ORDER])
+def test_alibi_softmax_tile_order(name, kw, sign, shape):
+    """ALiBi softmax at head dim 64 walks the key tiles from the last to the first and takes
+    the row max only on demand.  Steep slopes (up to 2 per key) with the standard sign put a
+    row's max on its first tile; the negated slopes put it on the last one, so the exact
+    fallback runs on almost every tile.  Prefix tiles come after the band tiles in that order.
     The smaller shape runs 2-wavefront workgroups, the larger 4-wavefront ones (PAIR, WIDE and
     WIDE2 steps)."""
     B, H, S = shape
-    D = 64
-    _say(f"[parity] rising scores {name} {shape}")
-    g = torch.Generator("cpu").manual_seed(S + len(name))
+    _say(f"[parity] alibi tile order {name} {shape}")
+    g = torch.Generator("cpu").manual_seed(S + 3 * len(name))
+    q, k, v = (torch.randn(B, H, S, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    slopes = [sign * 2.0 * 0.5 ** h for h in range(H)]
+    o = attention(q.to(DEV), k.to(DEV), v.to(DEV), alibi_slopes=slopes, **kw)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o).all()), f"{name}: non-finite output"
+    oc = o.float().cpu()
+    for b, h in {(0, 0), (0, H - 1), (B - 1, H // 2), (B // 2, 1 % H)}:
+        r = oracle.attention_ref(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1],
+                                 alibi_slopes=[slopes[h]], **kw)
+        res = gate.north_star_gate(r[0, 0], oc[b, h])
+        assert res.ok, f"{name} b={b} h={h}: {res.status} {res.stats}"
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("shape", [(1, 2, 512), (4, 16, 2048)], ids=["B1H2S512", "B4H16S2048"])
+@pytest.mark.parametrize("name,kw", RISING, ids=[r[0] for r in RISING])
+def test_softmax_rising_scores(name, kw, shape, D):
+    """Scores that rise along the keys: q ~ 4 sqrt(D/64) u, k_j ~ (j / 2) u (u a unit vector)
+    plus noise, so a row's max climbs ~23 log2-units per 64-key tile at either head dim.  The
+    softmax weights are first computed against the running reference max and, when a partial row
+    sum over a tile (paired core) or a 32-key step (one-block core) exceeds 2^16, recomputed
+    against the new max; these inputs take that path on almost every tile.  At head dim 64 the
+    smaller shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones
+    (PAIR, WIDE and WIDE2 steps), and the window / block masks run the one-block core; at head
+    dim 128 every case runs the one-block core."""
+    B, H, S = shape
+    _say(f"[parity] rising scores {name} {shape} D{D}")
+    g = torch.Generator("cpu").manual_seed(S + len(name) + D)
     u = torch.randn(D, generator=g)
     u = u / u.norm()
     ramp = torch.arange(S, dtype=torch.float32) * 0.5
     k = (ramp[:, None] * u + 0.3 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
-    q = (4.0 * u + 0.3 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
+    q = (4.0 * (D / 64) ** 0.5 * u + 0.3 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
     v = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
     kw = dict(kw)
     if kw.get("head_scale") == "per-head":
