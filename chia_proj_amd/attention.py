@@ -351,6 +351,36 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
                below 448; large softcaps or non-causal ALiBi distances can
                exceed it.
     Forward only."""
+    # Fast path, as in attention(): a call with the same shapes, layouts, formats
+    # and parameters as an earlier one reuses its argument structs; the data
+    # pointers and descales are new.
+    try:
+        key = ("fp8", q.shape, q.dtype, k.dtype, v.dtype, q.device, q.stride(), k.shape, k.stride(), v.shape,
+               v.stride(), k.device, v.device, None if out is None else (out.shape, out.dtype, out.device, out.stride()),
+               norm, causal, window, dilation, block, prefix, scale, softcap, bias, post_scale,
+               _head_key(head_scale), _head_key(alibi_slopes))
+    except (AttributeError, TypeError):
+        key = None
+    cache = _args_cache()
+    entry = cache.get(key) if key is not None else None
+    if entry is not None:
+        descales = (float(q_descale), float(k_descale), float(v_descale))
+        if all(d > 0 and math.isfinite(d) for d in descales):
+            a, f, hs, sl = entry
+            o = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device) if out is None else out
+            ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr())
+            if not (ptrs[0] | ptrs[1] | ptrs[2] | ptrs[3]) & 15:
+                a.q, a.k, a.v, a.o = ptrs
+                if hs is not None:
+                    a.head_scale = (head_scale if isinstance(head_scale, torch.Tensor) and head_scale.is_cuda
+                                    else hs).data_ptr()
+                if sl is not None:
+                    a.alibi_slopes = (alibi_slopes if isinstance(alibi_slopes, torch.Tensor) and alibi_slopes.is_cuda
+                                      else sl).data_ptr()
+                f.q_descale, f.k_descale, f.v_descale = descales
+                _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
+                return o
+
     _check_fp8(q, k, v, 4)
     B, H, S, D = q.shape
     if (k.shape != v.shape or k.shape[0] != B or k.shape[2:] != q.shape[2:] or k.shape[1] < 1
@@ -392,6 +422,13 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
                      k_descale=float(k_descale), v_descale=float(v_descale))
     with torch.cuda.device(q.device):
         _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
+    # cache the validated call when the tensors needed no layout change (o is
+    # always a fresh contiguous tensor or the caller's `out`, whose strides are
+    # part of the key)
+    if key is not None and q_ is q and k_ is k and v_ is v:
+        cache[key] = (a, f, hs, sl)
+        if len(cache) > _ARGS_CACHE_MAX:
+            cache.popitem(last=False)
     return o
 
 

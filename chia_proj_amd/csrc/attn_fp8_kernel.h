@@ -148,6 +148,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   // ALiBi without softcap seeds the QK^T accumulator with (sl / c1)(j - i): the
   // MFMA returns the biased score over c1 and the normalisers take their plain form.
   constexpr bool kBiasInit = ALIBI && !SOFTCAP;
+  // ALiBi softmax walks the key tiles from the last to the first: the bias grows
+  // with the key index, so a row's max is set on its first tile and O is rarely
+  // rescaled after it.
+  constexpr bool kRev = ALIBI && NORM == NORM_SOFTMAX;
   const float bq = kBiasInit ? sl / c1 : 0.0f;
 
   // this wavefront's 32 rows: Q as the MFMA B operand (lane = row, 32 bytes of d per 64)
@@ -194,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   const int v_key = 4 * hh + (t_src & 3) + 8 * (t_src >> 2);  // + 16 wp
 
   auto issue = [&](int it) {
-    const int jt0 = tile_at(tr, it) * BN;
+    const int jt0 = tile_at(tr, kRev ? ntiles - 1 - it : it) * BN;
     char* st = lds + (it % NS) * STAGE_BYTES;
     fp8_dma_rows<D>(kh, krs, jt0, g.S, st, wave, lane);
     fp8_dma_rows<D>(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
@@ -209,7 +213,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     asm volatile("" ::: "memory");
     if (dma_next < ntiles) issue(dma_next++);
     const char* St = lds + (it % NS) * STAGE_BYTES;
-    const int jt0 = tile_at(tr, it) * BN;
+    const int jt0 = tile_at(tr, kRev ? ntiles - 1 - it : it) * BN;
     const int cls = wvalid ? classify_tile(g, ra, rb, jt0, jt0 + BN - 1) : (int)TILE_EMPTY;
     if (cls == TILE_EMPTY) continue;
 

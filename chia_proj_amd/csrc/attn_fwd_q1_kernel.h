@@ -158,7 +158,14 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
   TileRange tr1{0, 0, 0};
   if (blk1 >= 0) tr1 = tile_range(g, blk1 * BM, imin32(blk1 * BM + BM - 1, g.S - 1), BN);
   const int nsteps = n0 + tr1.n_pre + tr1.n2;
-  auto step_key0 = [&](int s) { return (s < n0 ? tile_at(tr0, s) : tile_at(tr1, s - n0)) * BN; };
+  // ALiBi softmax walks each block's key tiles (and the two 32-key steps of a
+  // tile) from the last to the first: the bias grows with the key index, so
+  // a row's max is set on its first step and O is rarely rescaled after it.
+  constexpr bool kRev = ALIBI && NORM == NORM_SOFTMAX;
+  const int n1 = tr1.n_pre + tr1.n2;
+  auto step_key0 = [&](int s) {
+    return (s < n0 ? tile_at(tr0, kRev ? n0 - 1 - s : s) : tile_at(tr1, kRev ? n1 - 1 - (s - n0) : s - n0)) * BN;
+  };
 
   uint32_t k_dma[NDMA], v_dma[NDMA];
 #pragma unroll
@@ -266,10 +273,11 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
       asm volatile("" ::: "memory");
       if (dma_next < nsteps) issue_step(dma_next++);
       const char* St = lds + (step % NS) * STAGE_BYTES;
-      const int jt0 = tile_at(tr, it) * BN;
+      const int jt0 = tile_at(tr, kRev ? nt - 1 - it : it) * BN;
 
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kbs = 0; kbs < 2; ++kbs) {
+        const int kb = kRev ? 1 - kbs : kbs;
         const int jb = jt0 + 32 * kb;
         const int cls = key_class(jb, jb + 31);
         if (cls == TILE_EMPTY) continue;

@@ -166,3 +166,30 @@ def test_varlen_empty_and_rejections():
     ((q8, _), (k8, _), (v8, _)), cu = _packed([5, 7], 2, 2, 64, 2)
     with pytest.raises(ValueError):
         attention_fp8_varlen(q8.to(DEV), k8.to(DEV), v8.to(DEV), torch.tensor([0, 5, 11], dtype=torch.int32))
+
+
+def test_fp8_cached_launch_path_follows_new_data():
+    """Repeated attention_fp8 calls with one signature reuse the validated argument
+    structs: outputs must follow new tensors, new descales and in-place updates of a
+    device per-head vector, bit for bit against the same call on an empty cache."""
+    from chia_proj_amd.attention import _args_cache
+
+    _say("[fp8] cached launch path")
+    (q8, qd), (k8, kd), (v8, vd) = (tuple(x) for x in _inputs(1, 2, 2, 300, 64, 17))
+    (q2, q2d), _, _ = (tuple(x) for x in _inputs(1, 2, 2, 300, 64, 18))
+    qs, ks, vs, q2s = (t.to(DEV) for t in (q8, k8, v8, q2))
+    t = torch.tensor([0.5, 2.0], device=DEV)
+    kw = dict(causal=True, window=77, head_scale=t)
+    for qq, qqd, kscale, hmult in ((qs, qd, kd, 1.0), (q2s, q2d, kd, 1.0), (q2s, q2d, 0.5 * kd, 1.0),
+                                  (q2s, q2d, 0.5 * kd, 3.0)):
+        if hmult != 1.0:
+            t.mul_(hmult)  # same storage, new values
+        o = attention_fp8(qq, ks, vs, q_descale=qqd, k_descale=kscale, v_descale=vd, **kw)
+        torch.cuda.synchronize()
+        _args_cache().clear()
+        o_fresh = attention_fp8(qq, ks, vs, q_descale=qqd, k_descale=kscale, v_descale=vd, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_fresh)
+        # and the next call of the loop runs the cached path again
+        attention_fp8(qq, ks, vs, q_descale=qqd, k_descale=kscale, v_descale=vd, **kw)
+    _check("cached window 77", [(q2, q2d), (k8, 0.5 * kd), (v8, vd)], dict(causal=True, window=77, head_scale=t.cpu()))

@@ -166,22 +166,27 @@ ALIBI_ORDER = [
     ("prefix300", dict(causal=True, prefix=300), 1.0),
     ("causal_negative", dict(causal=True), -1.0),
     ("full_negative", dict(causal=False), -1.0),
+    ("window300", dict(causal=True, window=300), 1.0),
+    ("block256_negative", dict(causal=False, block=256), -1.0),
 ]
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("shape", [(1, 2, 700), (4, 16, 2048)], ids=["B1H2S700", "B4H16S2048"])
 @pytest.mark.parametrize("name,kw,sign", ALIBI_ORDER, ids=[a[0] for a in ALIBI_ORDER])
-def test_alibi_softmax_tile_order(name, kw, sign, shape):
-    """ALiBi softmax at head dim 64 walks the key tiles from the last to the first and takes
-    the row max only on demand.  Steep slopes (up to 2 per key) with the standard sign put a
-    row's max on its first tile; the negated slopes put it on the last one, so the exact
-    fallback runs on almost every tile.  Prefix tiles come after the band tiles in that order.
-    The smaller shape runs 2-wavefront workgroups, the larger 4-wavefront ones (PAIR, WIDE and
-    WIDE2 steps)."""
+def test_alibi_softmax_tile_order(name, kw, sign, shape, D):
+    """ALiBi softmax walks the key tiles from the last to the first (both cores; the paired
+    core also takes the row max only on demand).  Steep slopes (up to 2 per key) with the
+    standard sign put a row's max on its first tile; the negated slopes put it on the last one,
+    so the exact fallback (paired core) or the rescale (one-block core) runs on almost every
+    tile.  Prefix tiles come after the band tiles in that order.  At head dim 64 the smaller
+    shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones (PAIR,
+    WIDE and WIDE2 steps), and the window / block masks the one-block core; head dim 128 runs
+    the one-block core."""
     B, H, S = shape
-    _say(f"[parity] alibi tile order {name} {shape}")
-    g = torch.Generator("cpu").manual_seed(S + 3 * len(name))
-    q, k, v = (torch.randn(B, H, S, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    _say(f"[parity] alibi tile order {name} {shape} D{D}")
+    g = torch.Generator("cpu").manual_seed(S + 3 * len(name) + D)
+    q, k, v = (torch.randn(B, H, S, D, generator=g).to(torch.bfloat16) for _ in range(3))
     slopes = [sign * 2.0 * 0.5 ** h for h in range(H)]
     o = attention(q.to(DEV), k.to(DEV), v.to(DEV), alibi_slopes=slopes, **kw)
     torch.cuda.synchronize()
