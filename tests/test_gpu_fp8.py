@@ -193,3 +193,25 @@ def test_fp8_cached_launch_path_follows_new_data():
         # and the next call of the loop runs the cached path again
         attention_fp8(qq, ks, vs, q_descale=qqd, k_descale=kscale, v_descale=vd, **kw)
     _check("cached window 77", [(q2, q2d), (k8, 0.5 * kd), (v8, vd)], dict(causal=True, window=77, head_scale=t.cpu()))
+
+
+FP8_ALIBI_ORDER = [
+    ("causal", dict(causal=True), 1.0),
+    ("full", dict(causal=False), 1.0),
+    ("prefix200", dict(causal=True, prefix=200), 1.0),
+    ("causal_negative", dict(causal=True), -1.0),
+    ("window300_negative", dict(causal=False, window=300), -1.0),
+]
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("name,kw,sign", FP8_ALIBI_ORDER, ids=[a[0] for a in FP8_ALIBI_ORDER])
+def test_fp8_alibi_tile_order(name, kw, sign, D):
+    """The FP8 ALiBi softmax walks its key tiles from the last to the first.  Steep slopes (up to
+    1 per key) with the standard sign put a row's max on its first tile; negated slopes put it
+    on the last, so the running max moves (and O is rescaled) on nearly every tile; prefix tiles
+    come after the band tiles."""
+    _say(f"[fp8] alibi tile order {name} D{D}")
+    qkv = _inputs(1, 2, 2, 700, D, 29 + D + len(name))
+    kw = dict(kw, alibi_slopes=[sign * 1.0, sign * 0.125])
+    _check(f"alibi order {name} D{D}", qkv, kw)
