@@ -48,6 +48,8 @@ def _head_key(vals: PerHead):
                 raise TypeError("converted device vectors are not cached")  # caller takes the full path
             return ("dev", vals.data_ptr(), tuple(vals.shape))
         return ("host", tuple(vals.detach().reshape(-1).tolist()))
+    if type(vals) is tuple:  # e.g. the variants' cached presets: hashed as they are
+        return ("host", vals)
     return ("host", tuple(float(x) for x in vals))
 
 

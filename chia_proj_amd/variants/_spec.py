@@ -9,6 +9,7 @@ ALiBi slope h+1, temperature 0.5+h/H, softcap 30, causal sigmoid/ReLU).
 """
 from __future__ import annotations
 
+import functools
 from typing import Callable, Dict
 
 import torch
@@ -42,14 +43,24 @@ def standard_alibi_slopes(heads: int) -> torch.Tensor:
     return torch.tensor([2.0 ** (-8.0 * (h + 1) / heads) for h in range(heads)], dtype=torch.float32)
 
 
-def _per_head(vals, heads: int, default: Callable[[int], torch.Tensor]):
+@functools.lru_cache(maxsize=None)
+def _preset_values(name: str, heads: int) -> tuple:
+    """The float32 values of a per-head preset as a tuple of Python floats, built once per
+    head count: a variant call with the default passes these host values, which the launch
+    path keys by content, instead of building tensors on every call."""
+    fn = {"temperature": reference_temperature, "alibi": reference_alibi_slopes,
+          "standard": standard_alibi_slopes}[name]
+    return tuple(fn(heads).tolist())
+
+
+def _per_head(vals, heads: int, default: str):
     if vals is None:
-        return default(heads)
+        return _preset_values(default, heads)
     if isinstance(vals, str):
         if vals == "reference":
-            return default(heads)
+            return _preset_values(default, heads)
         if vals == "standard":
-            return standard_alibi_slopes(heads)
+            return _preset_values("standard", heads)
         raise ValueError(f"unknown per-head preset {vals!r}")
     return vals
 
@@ -75,8 +86,7 @@ def kw_prefix_lm(heads, *, prefix=256, scale=None):
 
 
 def kw_alibi(heads, *, slopes=None, causal=True, scale=None):
-    return dict(norm="softmax", causal=bool(causal), alibi_slopes=_per_head(slopes, heads, reference_alibi_slopes),
-                scale=scale)
+    return dict(norm="softmax", causal=bool(causal), alibi_slopes=_per_head(slopes, heads, "alibi"), scale=scale)
 
 
 def kw_softcap(heads, *, softcap=30.0, causal=True, scale=None):
@@ -84,15 +94,21 @@ def kw_softcap(heads, *, softcap=30.0, causal=True, scale=None):
 
 
 def kw_temperature(heads, *, temperature=None, mode="mul", causal=True, scale=None):
-    t = _per_head(temperature, heads, reference_temperature)
-    t = torch.as_tensor(t, dtype=torch.float32) if not isinstance(t, torch.Tensor) else t.to(torch.float32)
-    if mode == "mul":
-        hs = t
-    elif mode == "div":
-        hs = 1.0 / t
-    else:
+    if mode not in ("mul", "div"):
         raise ValueError(f"mode must be 'mul' or 'div', got {mode!r}")
+    if temperature is None or (isinstance(temperature, str) and temperature == "reference"):
+        hs = _preset_values("temperature", heads) if mode == "mul" else _reciprocal_temperature(heads)
+        return dict(norm="softmax", causal=bool(causal), head_scale=hs, scale=scale)
+    t = _per_head(temperature, heads, "temperature")
+    t = torch.as_tensor(t, dtype=torch.float32) if not isinstance(t, torch.Tensor) else t.to(torch.float32)
+    hs = t if mode == "mul" else 1.0 / t
     return dict(norm="softmax", causal=bool(causal), head_scale=hs, scale=scale)
+
+
+@functools.lru_cache(maxsize=None)
+def _reciprocal_temperature(heads: int) -> tuple:
+    """1 / t_h of the reference temperature, divided in float32 as for a tensor argument."""
+    return tuple((1.0 / torch.tensor(_preset_values("temperature", heads), dtype=torch.float32)).tolist())
 
 
 def kw_relu(heads, *, causal=True, post_scale=1.0, scale=None):
