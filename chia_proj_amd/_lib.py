@@ -171,6 +171,8 @@ _lock = threading.Lock()
 
 def _load():
     global _lib
+    if _lib is not None:  # loaded: no lock on the launch path
+        return _lib
     with _lock:
         if _lib is not None:
             return _lib
@@ -224,7 +226,7 @@ def status_string(status: int) -> str:
 
 
 def fwd(args: AttnArgs, stream: int) -> None:
-    st = _load().chia_attn_fwd(ctypes.byref(args), ctypes.c_void_p(stream))
+    st = _load().chia_attn_fwd(args, stream)  # argtypes pass the struct by reference
     if st != 0:
         raise ChiaAttnError(st, "chia_attn_fwd")
 
@@ -236,7 +238,7 @@ def fwd_lse(args: AttnArgs, lse_ptr: int, stream: int) -> None:
 
 
 def fwd_fp8(args: Fp8Args, stream: int) -> None:
-    st = _load().chia_attn_fwd_fp8(ctypes.byref(args), ctypes.c_void_p(stream))
+    st = _load().chia_attn_fwd_fp8(args, stream)  # argtypes pass the struct by reference
     if st != 0:
         raise ChiaAttnError(st, "chia_attn_fwd_fp8")
 

@@ -27,6 +27,16 @@ SUPPORTED_HEAD_DIMS = (64, 128)
 _VEC_CACHE_MAX = 64
 _vec_cache: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
 _ARGS_CACHE_MAX = 256
+
+# The current stream's raw handle for a device index, without building a Stream
+# object (the cached launch paths' largest fixed cost after the launch itself).
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _current_stream(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
 _tls = threading.local()
 
 
@@ -180,7 +190,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, norm: str = 
             if sl is not None:
                 a.alibi_slopes = (alibi_slopes if isinstance(alibi_slopes, torch.Tensor) and alibi_slopes.is_cuda
                                   else sl).data_ptr()
-            _lib.fwd(a, torch.cuda.current_stream(q.device).cuda_stream)
+            _lib.fwd(a, _current_stream(q))
             return o
 
     a, hs, sl, (q_, k_, v_), o = _prepare(q, k, v, out, **params)
@@ -380,7 +390,7 @@ def attention_fp8(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, q_descal
                     a.alibi_slopes = (alibi_slopes if isinstance(alibi_slopes, torch.Tensor) and alibi_slopes.is_cuda
                                       else sl).data_ptr()
                 f.q_descale, f.k_descale, f.v_descale = descales
-                _lib.fwd_fp8(f, torch.cuda.current_stream(q.device).cuda_stream)
+                _lib.fwd_fp8(f, _current_stream(q))
                 return o
 
     _check_fp8(q, k, v, 4)
