@@ -376,8 +376,39 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     }
   }
 
+  // ---- key intervals of every wavefront's blocks, evaluated in lanes ---------
+  // Lane l works for wavefront w = l % NW: the interval ends key_lo / key_hi
+  // at the first (a) and last (b) row of w's two query blocks, and w's fast
+  // ranges.  A wavefront reads its own values from lane `wave`, and the
+  // workgroup's tile range and WIDE2 range from lanes 0..NW-1, so this set-up
+  // runs as a handful of vector instructions instead of some thousand scalar
+  // ones (the scalar unit is shared by every wavefront of the CU).
+  int lk[QB][4];  // key_lo(a), key_hi(b), key_lo(b), key_hi(a)
+  FastRanges lf;
+  {
+    const int lw = lane & (NW - 1);
+    int la[QB];
+    bool lv[QB];
+    la[0] = blk0 * BMH + 32 * lw;
+    la[1] = (blk1 >= 0 ? blk1 : blk0) * BMH + 32 * lw;
+    lv[0] = la[0] < g.S;
+    lv[1] = blk1 >= 0 && la[1] < g.S;
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      const int lb = imin32(la[qb] + 31, g.S - 1);
+      lk[qb][0] = key_lo(g, la[qb]);
+      lk[qb][1] = key_hi(g, lb);
+      lk[qb][2] = key_lo(g, lb);
+      lk[qb][3] = key_hi(g, la[qb]);
+    }
+    lf = fast_ranges_keys(g.S, lk[0][2], lk[0][3], lk[0][0], lk[0][1], lv[0], lk[1][2], lk[1][3], lv[1], BN);
+  }
+
   // ---- KV tiles this workgroup visits ---------------------------------------
-  const TileRange tr = tile_range(g, blk0 * BMH, imin32((blk1 >= 0 ? blk1 : blk0) * BMH + BMH - 1, g.S - 1), BN);
+  // hull of the workgroup's rows: from the first row of wavefront 0's block 0
+  // to the last row of wavefront NW-1's block 1 (block 0 when there is none)
+  const TileRange tr =
+      tile_range_keys(g, __builtin_amdgcn_readlane(lk[0][0], 0), __builtin_amdgcn_readlane(lk[1][1], NW - 1), BN);
   const int ntiles = tr.n_pre + tr.n2;
   // the tile of step k, and whether it lies in the band (not the prefix)
   auto seq_tile = [&](int k) __attribute__((always_inline)) { return tile_at(tr, kRev ? ntiles - 1 - k : k); };
@@ -474,11 +505,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   int c_ulo[QB], c_uhi[QB], c_ilo[QB], c_ihi[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
-    const int a = row0[qb], b = imin32(row0[qb] + 31, g.S - 1);
-    c_ulo[qb] = key_lo(g, a);
-    c_uhi[qb] = key_hi(g, b);
-    c_ilo[qb] = key_lo(g, b);
-    c_ihi[qb] = key_hi(g, a);
+    c_ulo[qb] = __builtin_amdgcn_readlane(lk[qb][0], wave);
+    c_uhi[qb] = __builtin_amdgcn_readlane(lk[qb][1], wave);
+    c_ilo[qb] = __builtin_amdgcn_readlane(lk[qb][2], wave);
+    c_ihi[qb] = __builtin_amdgcn_readlane(lk[qb][3], wave);
   }
   auto tile_class = [&](int qb, int c, int d) {
     if (!valid[qb]) return (int)TILE_EMPTY;
@@ -760,12 +790,19 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // ---- main loop -------------------------------------------------------------
   // Band tiles whose class is known without classifying (both blocks FULL,
   // or block 0 done and block 1 FULL); everything else is classified.
-  const FastRanges fr = fast_ranges(g, row0[0], imin32(row0[0] + 31, g.S - 1), valid[0], row0[1],
-                                    imin32(row0[1] + 31, g.S - 1), valid[1], BN);
+  const FastRanges fr{__builtin_amdgcn_readlane(lf.pf_lo, wave), __builtin_amdgcn_readlane(lf.pf_hi, wave),
+                      __builtin_amdgcn_readlane(lf.wf_lo, wave), __builtin_amdgcn_readlane(lf.wf_hi, wave)};
   // WIDE2 tiles: block 0 done and block 1 FULL in every wavefront, since a
-  // WIDE2 step changes the barrier count.
+  // WIDE2 step changes the barrier count (wide_range_all, from the lanes).
   TileSpan w2{1, 0};
-  if constexpr (kWide2) w2 = wide_range_all(g, blk0 * BMH, (blk1 >= 0 ? blk1 : blk0) * BMH, blk1 >= 0, NW, BN);
+  if constexpr (kWide2) {
+    w2 = TileSpan{0, 0x7fffffff};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      w2.lo = imax32(w2.lo, __builtin_amdgcn_readlane(lf.wf_lo, w));
+      w2.hi = imin32(w2.hi, __builtin_amdgcn_readlane(lf.wf_hi, w));
+    }
+  }
 
   // ---- pipelined run over the tiles both blocks see in full -----------------
   // A step is one 32-key block kb of a tile for both query blocks (two 32 x 32

@@ -141,26 +141,33 @@ struct FastRanges {
   int32_t pf_lo, pf_hi, wf_lo, wf_hi;
 };
 
-CHIA_HD FastRanges fast_ranges(const MaskGeom& g, int32_t a0, int32_t b0, bool v0, int32_t a1, int32_t b1, bool v1,
-                               int32_t bn) {
+// The same from the blocks' interval ends: for block 0, ilo0 = key_lo(b0),
+// ihi0 = key_hi(a0), ulo0 = key_lo(a0), uhi0 = key_hi(b0); for block 1,
+// ilo1 = key_lo(b1), ihi1 = key_hi(a1).  S is the sub-sequence length.
+CHIA_HD FastRanges fast_ranges_keys(int32_t S, int32_t ilo0, int32_t ihi0, int32_t ulo0, int32_t uhi0, bool v0,
+                                    int32_t ilo1, int32_t ihi1, bool v1, int32_t bn) {
   FastRanges r{1, 0, 1, 0};
   // FULL band tiles of a block: c >= key_lo(b), d <= key_hi(a), d <= S - 1
-  const int32_t ilo0 = key_lo(g, b0), ihi0 = key_hi(g, a0), ilo1 = key_lo(g, b1), ihi1 = key_hi(g, a1);
   const bool f0 = v0 && ilo0 <= ihi0, f1 = v1 && ilo1 <= ihi1;
-  const int32_t lo0 = ceil_div(ilo0, bn), hi0 = imin32(floor_div(ihi0 + 1, bn), g.S / bn) - 1;
-  const int32_t lo1 = ceil_div(ilo1, bn), hi1 = imin32(floor_div(ihi1 + 1, bn), g.S / bn) - 1;
+  const int32_t lo0 = ceil_div(ilo0, bn), hi0 = imin32(floor_div(ihi0 + 1, bn), S / bn) - 1;
+  const int32_t lo1 = ceil_div(ilo1, bn), hi1 = imin32(floor_div(ihi1 + 1, bn), S / bn) - 1;
   if (f0 && f1) {
     r.pf_lo = imax32(lo0, lo1);
     r.pf_hi = imin32(hi0, hi1);
   }
   if (f1) {
     // block 0 sees no key after its hull end key_hi(b0)
-    const int32_t ulo0 = key_lo(g, a0), uhi0 = key_hi(g, b0);
     const int32_t after0 = (v0 && ulo0 <= uhi0) ? uhi0 / bn + 1 : 0;
     r.wf_lo = imax32(lo1, after0);
     r.wf_hi = hi1;
   }
   return r;
+}
+
+CHIA_HD FastRanges fast_ranges(const MaskGeom& g, int32_t a0, int32_t b0, bool v0, int32_t a1, int32_t b1, bool v1,
+                               int32_t bn) {
+  return fast_ranges_keys(g.S, key_lo(g, b0), key_hi(g, a0), key_lo(g, a0), key_hi(g, b0), v0, key_lo(g, b1),
+                          key_hi(g, a1), v1, bn);
 }
 
 // Band tiles in the WIDE range of every wavefront of a workgroup: wavefront w
@@ -217,10 +224,10 @@ struct TileRange {
   int32_t n_pre, start2, n2;
 };
 
-CHIA_HD TileRange tile_range(const MaskGeom& g, int32_t a, int32_t b, int32_t bn) {
+// The same from the hull ends ulo = key_lo(g, a), uhi = key_hi(g, b).
+CHIA_HD TileRange tile_range_keys(const MaskGeom& g, int32_t ulo, int32_t uhi, int32_t bn) {
   TileRange t;
   t.n_pre = (g.prefix + bn - 1) / bn;
-  const int32_t ulo = key_lo(g, a), uhi = key_hi(g, b);
   t.start2 = t.n_pre;
   t.n2 = 0;
   if (ulo <= uhi) {
@@ -229,6 +236,10 @@ CHIA_HD TileRange tile_range(const MaskGeom& g, int32_t a, int32_t b, int32_t bn
     t.n2 = imax32(0, t1 - t.start2 + 1);
   }
   return t;
+}
+
+CHIA_HD TileRange tile_range(const MaskGeom& g, int32_t a, int32_t b, int32_t bn) {
+  return tile_range_keys(g, key_lo(g, a), key_hi(g, b), bn);
 }
 
 CHIA_HD int32_t tile_at(const TileRange& t, int32_t k) {
