@@ -1,8 +1,9 @@
 """CPU checks of chia_proj_amd/csrc/mask.h by brute force: the kernel's
 unclassified fast paths (fast_ranges, wide_range_all) against classify_tile over
 masks, residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp), and
-the multiply-high divider against plain division (tests/cpp/check_udiv.cpp) and
-the LDS tile layout against a bank model (tests/cpp/check_lds_banks.cpp), all
+the multiply-high divider against plain division (tests/cpp/check_udiv.cpp),
+the LDS tile layout against a bank model (tests/cpp/check_lds_banks.cpp) and
+the paired core's DMA / barrier schedule (tests/cpp/check_schedule.cpp), all
 built with AddressSanitizer and UndefinedBehaviorSanitizer."""
 import shutil
 import subprocess
@@ -44,3 +45,20 @@ def test_lds_layout_is_bank_conflict_free(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "0 failures" in out.stdout
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_tile_schedule_is_safe(tmp_path):
+    """The paired core's tile schedule (prologue, WIDE2 steps, pipelined run,
+    vmcnt waits, stage reuse) over every workgroup of a mask and shape sweep:
+    equal barriers in every wavefront, every read tile landed, no stage reused
+    while read; and each of four planted schedule mistakes is caught."""
+    exe = tmp_path / "check_schedule"
+    subprocess.run(["g++", "-std=c++17", "-O1", *SANITIZE, f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+                    str(ROOT / "tests" / "cpp" / "check_schedule.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "0 violations" in out.stdout
+    planted = subprocess.run([str(exe), "planted"], capture_output=True, text=True)
+    assert planted.returncode == 0, planted.stdout + planted.stderr
+    assert planted.stdout.count("planted mistake") == 4
