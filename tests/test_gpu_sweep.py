@@ -11,7 +11,14 @@ output against the generic oracle (oracle/generic.py::attention_ref), so the
 combinations that no hand-written case names are covered too.  The large cases
 (2-4 sequences, 32-64 heads, S 2048-3000) fill enough workgroups for the 4-wavefront kernels
 (WIDE2 steps, the pipelined run, the backwards ALiBi walk); they check every
-output is finite and gate three sampled heads.
+output is finite and gate three sampled heads.  The same draws also drive the
+FP8 forward (e4m3 or e5m2 inputs, against oracle/fp8.py under the FP8 suite's
+gate) and the backward (gradients through attention()'s autograd path, against
+oracle/grad.py under the backward suite's gate).  For softmax the backward's
+gate also allows twice the error of oracle/grad.py's fused-backward rounding
+model: a fused backward takes the row term do . o from the bf16 output o, and
+where a row sees a few keys of similar dP that rounding alone reaches 1-2 % of
+the largest gradient (a causal window of 2 under grouped-query K/V, say).
 """
 import random
 
@@ -19,13 +26,19 @@ import pytest
 import torch
 
 import oracle
-from chia_proj_amd import attention, gate
+from chia_proj_amd import attention, attention_fp8, gate, quantize_fp8
+from oracle.fp8 import fp8_emulated, fp8_ref
+from oracle.grad import attention_grad_flash_model, attention_grad_ref
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 N_CASES = 200
 N_LARGE = 32
+N_FP8 = 64
+N_BWD = 48
+GRAD_MAX = 1e-2  # the backward suite's gate (tests/test_gpu_backward.py)
+GRAD_MEAN = 1e-3
 
 
 def _draw(seed, large=False):
@@ -113,3 +126,53 @@ def test_random_forward_case_large(seed):
         ref = oracle.attention_ref(q[b:b + 1, h:h + 1], k[b:b + 1, kv:kv + 1], v[b:b + 1, kv:kv + 1], **one)
         res = gate.north_star_gate(ref[0, 0], oc[b, h], scale_aware=kw["norm"] != "softmax")
         assert res.ok, f"large seed {seed} b={b} h={h}: {res.status} {res.stats}"
+
+
+
+@pytest.mark.parametrize("seed", range(N_FP8))
+def test_random_fp8_case(seed):
+    B, H, Hkv, S, D, kw, _ = _draw(20261204 + seed)
+    fmt = torch.float8_e5m2 if seed % 3 == 2 else torch.float8_e4m3fn
+    print(f"[sweep] fp8 seed {seed}: {fmt} B{B} H{H}/{Hkv} S{S} D{D} {kw}", flush=True)
+    g = torch.Generator("cpu").manual_seed(2000 + seed)
+    (q8, qd), (k8, kd), (v8, vd) = (quantize_fp8(torch.randn(B, h, S, D, generator=g), dtype=fmt) for h in (H, Hkv, Hkv))
+    o = attention_fp8(q8.to(DEV), k8.to(DEV), v8.to(DEV), q_descale=qd, k_descale=kd, v_descale=vd, **kw)
+    torch.cuda.synchronize()
+    got = o.float().cpu()
+    assert o.shape == (B, H, S, D) and bool(torch.isfinite(got).all())
+    ref = fp8_ref(q8, k8, v8, qd, kd, vd, **kw)
+    emu = fp8_emulated(q8, k8, v8, qd, kd, vd, **kw)
+    # the FP8 suite's gate (tests/test_gpu_fp8.py): twice the rounding model's error plus the bf16 gate
+    for b in range(B):
+        for h in range(H):
+            r = ref[b, h]
+            sc = max(1.0, r.abs().max().item())
+            e_k, e_m = (got[b, h] - r).abs(), (emu[b, h] - r).abs()
+            assert e_k.max().item() <= 2 * e_m.max().item() + 2e-2 * sc, (seed, b, h, e_k.max().item())
+            assert e_k.mean().item() <= 2 * e_m.mean().item() + 2e-3 * sc, (seed, b, h, e_k.mean().item())
+
+
+@pytest.mark.parametrize("seed", range(N_BWD))
+def test_random_backward_case(seed):
+    B, H, Hkv, S, D, kw, strided = _draw(20261205 + seed)
+    S = min(S, 320)  # the gradient oracle is an autograd pass over S x S
+    print(f"[sweep] bwd seed {seed}: B{B} H{H}/{Hkv} S{S} D{D} {kw} strided={strided}", flush=True)
+    g = torch.Generator("cpu").manual_seed(3000 + seed)
+    q, k, v = (torch.randn(B, h, S, D, generator=g).to(torch.bfloat16) for h in (H, Hkv, Hkv))
+    do = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    if strided:  # interleaved heads in memory
+        qg = q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2).requires_grad_(True)
+    o = attention(qg, kg, vg, **kw)
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    refs = attention_grad_ref(q, k, v, do, **kw)
+    models = attention_grad_flash_model(q, k, v, do, **kw) if kw["norm"] == "softmax" else refs
+    floor = 1e-3 * max(r.abs().max().item() for r in refs)
+    for label, got, r, mdl in zip(("dq", "dk", "dv"), (qg.grad, kg.grad, vg.grad), refs, models):
+        assert bool(torch.isfinite(got.float()).all()), (seed, label)
+        err = (got.float().cpu() - r).abs()
+        e_m = (mdl.float() - r).abs()
+        m = max(r.abs().max().item(), floor, 1e-30)
+        assert err.max().item() <= 2 * e_m.max().item() + GRAD_MAX * m, (seed, label, err.max().item() / m)
+        assert err.mean().item() <= 2 * e_m.mean().item() + GRAD_MEAN * m, (seed, label, err.mean().item() / m)

@@ -5,14 +5,17 @@ own holds gradients; the pins are:
   * finite differences (torch.autograd.gradcheck, float64) for every kind of
     mask, score modifier and normaliser, and for grouped-query K/V;
   * torch's own scaled_dot_product_attention backward (an independent
-    implementation) for softmax masks, with and without enable_gqa.
+    implementation) for softmax masks, with and without enable_gqa;
+  * the fused-backward rounding model (attention_grad_flash_model): without
+    its rounding it equals the autograd gradients in float64 (so its stated
+    softmax backward is right), and its rounding moves dq and dk only.
 """
 import pytest
 import torch
 import torch.nn.functional as F
 
 from oracle.generic import attention_ref, visible_mask
-from oracle.grad import attention_grad_ref, attention_out_diff
+from oracle.grad import attention_grad_flash_model, attention_grad_ref, attention_out_diff
 
 CASES = [
     dict(causal=True),
@@ -71,3 +74,31 @@ def test_softmax_gradient_equals_sdpa_backward(kw, H, Hkv):
     o.backward(do)
     for g_got, g_want in zip(got, (qs.grad, ks.grad, vs.grad)):
         torch.testing.assert_close(g_got, g_want, rtol=1e-10, atol=1e-10)
+
+
+SOFTMAX_CASES = [c for c in CASES if c.get("norm", "softmax") == "softmax"]
+
+
+@pytest.mark.parametrize("kw", SOFTMAX_CASES, ids=[str(c) for c in SOFTMAX_CASES])
+@pytest.mark.parametrize("H,Hkv", [(2, 2), (4, 1)])
+def test_flash_model_without_rounding_is_autograd(kw, H, Hkv):
+    q, k, v = _inputs(H=H, Hkv=Hkv, S=20, D=8, seed=11)
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(12), dtype=torch.float64)
+    kw = {key: (val * (H // 2) if isinstance(val, list) else val) for key, val in kw.items()}  # per-head lists
+    want = attention_grad_ref(q, k, v, do, dtype=torch.float64, **kw)
+    got = attention_grad_flash_model(q, k, v, do, round_o=False, **kw)
+    for g, w in zip(got, want):
+        torch.testing.assert_close(g, w, rtol=1e-10, atol=1e-12)
+
+
+def test_flash_model_rounding_moves_dq_dk_only():
+    """The row term enters dS, so dq and dk move by at most the bf16 rounding of
+    o times the size of do and the other operand; dv = P^T do does not move."""
+    q, k, v = _inputs(H=2, Hkv=1, S=24, D=8, seed=13)
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(14), dtype=torch.float64)
+    exact = attention_grad_ref(q, k, v, do, dtype=torch.float64, causal=True, window=2)
+    model = attention_grad_flash_model(q, k, v, do, causal=True, window=2)
+    torch.testing.assert_close(model[2], exact[2], rtol=0, atol=1e-12)
+    for g, w in zip(model[:2], exact[:2]):
+        moved = (g - w).abs().max().item()
+        assert 0 < moved <= 2.0 ** -6 * w.abs().max().item()
