@@ -33,10 +33,10 @@ from oracle.grad import attention_grad_flash_model, attention_grad_ref
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-N_CASES = 200
+N_CASES = 400
 N_LARGE = 32
-N_FP8 = 64
-N_BWD = 48
+N_FP8 = 128
+N_BWD = 96
 GRAD_MAX = 1e-2  # the backward suite's gate (tests/test_gpu_backward.py)
 GRAD_MEAN = 1e-3
 
