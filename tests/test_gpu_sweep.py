@@ -19,6 +19,8 @@ gate also allows twice the error of oracle/grad.py's fused-backward rounding
 model: a fused backward takes the row term do . o from the bf16 output o, and
 where a row sees a few keys of similar dP that rounding alone reaches 1-2 % of
 the largest gradient (a causal window of 2 under grouped-query K/V, say).
+Packed batches of 1-7 random-length sequences (empty ones included) go through
+attention_varlen, each sequence gated against the oracle on its own slice.
 """
 import random
 
@@ -26,7 +28,8 @@ import pytest
 import torch
 
 import oracle
-from chia_proj_amd import attention, attention_fp8, gate, quantize_fp8
+from oracle.generic import attention_ref
+from chia_proj_amd import attention, attention_fp8, attention_varlen, gate, quantize_fp8
 from oracle.fp8 import fp8_emulated, fp8_ref
 from oracle.grad import attention_grad_flash_model, attention_grad_ref
 
@@ -37,6 +40,7 @@ N_CASES = 400
 N_LARGE = 32
 N_FP8 = 128
 N_BWD = 96
+N_VARLEN = 64
 GRAD_MAX = 1e-2  # the backward suite's gate (tests/test_gpu_backward.py)
 GRAD_MEAN = 1e-3
 
@@ -176,3 +180,33 @@ def test_random_backward_case(seed):
         m = max(r.abs().max().item(), floor, 1e-30)
         assert err.max().item() <= 2 * e_m.max().item() + GRAD_MAX * m, (seed, label, err.max().item() / m)
         assert err.mean().item() <= 2 * e_m.mean().item() + GRAD_MEAN * m, (seed, label, err.mean().item() / m)
+
+
+@pytest.mark.parametrize("seed", range(N_VARLEN))
+def test_random_varlen_case(seed):
+    _, H, Hkv, S, D, kw, _ = _draw(20261206 + seed)
+    rnd = random.Random(seed)
+    lens = [rnd.choice([0, rnd.randint(1, 40), rnd.randint(1, S)]) for _ in range(rnd.randint(1, 7))]
+    if sum(lens) == 0:
+        lens[0] = 1
+    print(f"[sweep] varlen seed {seed}: lens {lens} H{H}/{Hkv} D{D} {kw}", flush=True)
+    g = torch.Generator("cpu").manual_seed(4000 + seed)
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    k, v = (torch.randn(T, Hkv, D, generator=g).to(torch.bfloat16) for _ in range(2))
+    cu = [0]
+    for L in lens:
+        cu.append(cu[-1] + L)
+    o = attention_varlen(q.to(DEV), k.to(DEV), v.to(DEV), torch.tensor(cu, dtype=torch.int32, device=DEV), **kw)
+    torch.cuda.synchronize()
+    o = o.float().cpu()
+    assert bool(torch.isfinite(o).all())
+    seq = lambda t, b: t[cu[b]:cu[b + 1]].transpose(0, 1).unsqueeze(0)  # noqa: E731  [1, H, S_b, D]
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        ref = attention_ref(seq(q, b), seq(k, b), seq(v, b), **kw)
+        got = seq(o, b)
+        for h in range(H):
+            res = gate.north_star_gate(ref[0, h], got[0, h], scale_aware=kw["norm"] != "softmax")
+            assert res.ok, (seed, b, h, res.status, res.stats)
