@@ -20,7 +20,9 @@ model: a fused backward takes the row term do . o from the bf16 output o, and
 where a row sees a few keys of similar dP that rounding alone reaches 1-2 % of
 the largest gradient (a causal window of 2 under grouped-query K/V, say).
 Packed batches of 1-7 random-length sequences (empty ones included) go through
-attention_varlen, each sequence gated against the oracle on its own slice.
+attention_varlen, each sequence gated against the oracle on its own slice; their
+gradients likewise; and the FP8 packed launch must give each sequence the bits of
+attention_fp8 on that sequence alone.
 """
 import random
 
@@ -29,7 +31,7 @@ import torch
 
 import oracle
 from oracle.generic import attention_ref
-from chia_proj_amd import attention, attention_fp8, attention_varlen, gate, quantize_fp8
+from chia_proj_amd import attention, attention_fp8, attention_fp8_varlen, attention_varlen, gate, quantize_fp8
 from oracle.fp8 import fp8_emulated, fp8_ref
 from oracle.grad import attention_grad_flash_model, attention_grad_ref
 
@@ -41,6 +43,8 @@ N_LARGE = 32
 N_FP8 = 128
 N_BWD = 96
 N_VARLEN = 64
+N_VARLEN_BWD = 32
+N_VARLEN_FP8 = 32
 GRAD_MAX = 1e-2  # the backward suite's gate (tests/test_gpu_backward.py)
 GRAD_MEAN = 1e-3
 
@@ -210,3 +214,70 @@ def test_random_varlen_case(seed):
         for h in range(H):
             res = gate.north_star_gate(ref[0, h], got[0, h], scale_aware=kw["norm"] != "softmax")
             assert res.ok, (seed, b, h, res.status, res.stats)
+
+
+def _lens(rnd, S):
+    lens = [rnd.choice([0, rnd.randint(1, 40), rnd.randint(1, S)]) for _ in range(rnd.randint(1, 7))]
+    if sum(lens) == 0:
+        lens[0] = 1
+    return lens
+
+
+@pytest.mark.parametrize("seed", range(N_VARLEN_BWD))
+def test_random_varlen_backward_case(seed):
+    _, H, Hkv, S, D, kw, _ = _draw(20261207 + seed)
+    rnd = random.Random(seed)
+    lens = _lens(rnd, min(S, 200))
+    print(f"[sweep] varlen bwd seed {seed}: lens {lens} H{H}/{Hkv} D{D} {kw}", flush=True)
+    g = torch.Generator("cpu").manual_seed(5000 + seed)
+    T = sum(lens)
+    q = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    k, v = (torch.randn(T, Hkv, D, generator=g).to(torch.bfloat16) for _ in range(2))
+    do = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    cu = [0]
+    for L in lens:
+        cu.append(cu[-1] + L)
+    qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    o = attention_varlen(qg, kg, vg, torch.tensor(cu, dtype=torch.int32, device=DEV), **kw)
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    grads = [t.grad.float().cpu() for t in (qg, kg, vg)]
+    seq = lambda t, b: t[cu[b]:cu[b + 1]].transpose(0, 1).unsqueeze(0)  # noqa: E731  [1, H, S_b, D]
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        sl = [seq(t, b) for t in (q, k, v, do)]
+        refs = attention_grad_ref(*sl, **kw)
+        models = attention_grad_flash_model(*sl, **kw) if kw["norm"] == "softmax" else refs
+        floor = 1e-3 * max(r.abs().max().item() for r in refs)
+        for label, got, r, mdl in zip(("dq", "dk", "dv"), grads, refs, models):
+            gb = seq(got, b)
+            assert bool(torch.isfinite(gb).all()), (seed, b, label)
+            err, e_m = (gb - r).abs(), (mdl.float() - r).abs()
+            m = max(r.abs().max().item(), floor, 1e-30)
+            assert err.max().item() <= 2 * e_m.max().item() + GRAD_MAX * m, (seed, b, label, err.max().item() / m)
+            assert err.mean().item() <= 2 * e_m.mean().item() + GRAD_MEAN * m, (seed, b, label)
+
+
+@pytest.mark.parametrize("seed", range(N_VARLEN_FP8))
+def test_random_fp8_varlen_case(seed):
+    _, H, Hkv, S, D, kw, _ = _draw(20261208 + seed)
+    rnd = random.Random(seed)
+    lens = _lens(rnd, S)
+    fmt = torch.float8_e5m2 if seed % 3 == 2 else torch.float8_e4m3fn
+    print(f"[sweep] fp8 varlen seed {seed}: {fmt} lens {lens} H{H}/{Hkv} D{D} {kw}", flush=True)
+    g = torch.Generator("cpu").manual_seed(6000 + seed)
+    T = sum(lens)
+    (q8, qd), (k8, kd), (v8, vd) = (quantize_fp8(torch.randn(T, h, D, generator=g), dtype=fmt) for h in (H, Hkv, Hkv))
+    cu = [0]
+    for L in lens:
+        cu.append(cu[-1] + L)
+    o = attention_fp8_varlen(q8.to(DEV), k8.to(DEV), v8.to(DEV), torch.tensor(cu, dtype=torch.int32, device=DEV),
+                             q_descale=qd, k_descale=kd, v_descale=vd, **kw)
+    torch.cuda.synchronize()
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        one = lambda t: t[cu[b]:cu[b + 1]].permute(1, 0, 2).unsqueeze(0).contiguous().to(DEV)  # noqa: E731
+        alone = attention_fp8(one(q8), one(k8), one(v8), q_descale=qd, k_descale=kd, v_descale=vd, **kw)
+        assert torch.equal(o[cu[b]:cu[b + 1]], alone[0].permute(1, 0, 2)), (seed, b)
