@@ -233,19 +233,28 @@ A100_PUBLISHED_US = {
 }
 
 
-def reference_report(dev, args) -> int:
-    """All ten variants at the reference's benchmark shape and constants (B2 H32 S2048
-    D128, extra_bench.py:5,32-62), called through the glob-compatible <op>_BEST.py
-    modules loaded as extra_bench.py:24-27 loads them; HIP-event median and cold-cache
-    us/call beside the reference's published A100 latencies (context, not a target)."""
+# The reference's published A100 sequence sweep (results/FINAL_seqsweep.csv:2-31,
+# GraphSynth kernels at B2 H32 D128): us/call where its status is "generalises",
+# None where its kernel failed at that S ("AssertionError").  Context only.
+A100_SEQSWEEP_US = {
+    "sigmoid_attn": {1024: 312.5, 2048: 1074.1, 4096: 4343.5},
+    "relu_attn": {1024: 151.0, 2048: 472.5, 4096: 1662.1},
+    "temp_perhead": {1024: 530.2, 2048: 1867.4, 4096: 6892.3},
+    "bias_alibi": {1024: 227.5, 2048: 843.1, 4096: 3222.8},
+    "bias_dilated": {1024: 497.9, 2048: 1818.2, 4096: 7136.2},
+    "bias_local": {1024: None, 2048: 663.0, 4096: None},
+    "bias_block_diagonal": {1024: None, 2048: 289.8, 4096: None},
+    "bias_prefix_lm": {1024: 663.8, 2048: 1389.6, 4096: 9608.3},
+    "softcap_gemma2": {1024: 262.9, 2048: 900.9, 4096: 3329.6},
+    "bias_sliding_window": {1024: None, 2048: 432.9, 4096: None},
+}
+
+
+def _load_best_modules():
+    """op -> launch_kernel of the glob-compatible <op>_BEST.py modules, found and
+    loaded as extra_bench.py:24-27,65-70 does."""
     import glob
     import importlib.util
-
-    import torch
-
-    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, rates
-    from chia_proj_amd.timing import CacheFlusher, cold_us, median_us
-    from chia_proj_amd.workloads import draw_inputs, reference_suite
 
     loaded = {}
     for path in glob.glob(str(REPO / "chia_proj_amd" / "kernels_mi355x" / "*_BEST.py")):
@@ -255,43 +264,76 @@ def reference_report(dev, args) -> int:
         mod = importlib.util.module_from_spec(spec)
         spec.loader.exec_module(mod)
         loaded[op] = mod.launch_kernel
-    from chia_proj_amd.accounting import work
+    return loaded
 
-    cases = reference_suite()
-    q, k, v, _ = draw_inputs(cases[0], dev)
+
+def reference_report(dev, args) -> int:
+    """All ten variants at the reference's benchmark shape and constants (B2 H32 D128,
+    extra_bench.py:5,32-62), called through the glob-compatible <op>_BEST.py modules
+    loaded as extra_bench.py:24-27 loads them; HIP-event median and cold-cache us/call
+    beside the reference's published A100 latencies (context, not a target).
+    Suite "reference" is its benchmark at S = 2048 (FINAL_flexattention.csv);
+    suite "seqsweep" its sequence sweep at S = 1024, 2048, 4096 (extra_bench.py:166-201,
+    FINAL_seqsweep.csv), one q, k, v draw per S shared by the ten variants."""
+    import torch
+
+    from chia_proj_amd.accounting import PEAK_BF16_TFLOPS, rates, work
+    from chia_proj_amd.timing import CacheFlusher, cold_us, median_us
+    from chia_proj_amd.workloads import REFERENCE_SWEEP_S, draw_inputs, reference_suite
+
+    sweep = args.suite == "seqsweep"
+    seq_lens = REFERENCE_SWEEP_S if sweep else (2048,)
+    loaded = _load_best_modules()
     flusher = CacheFlusher(device=dev)
-    if args.pmc_mode:  # for rocprofv3 --pmc: each variant twice after a cache flush, nothing timed
-        for c in cases:
-            for _ in range(2):
-                flusher()
-                loaded[c.op](q, k, v)
-        torch.cuda.synchronize()
-        print(json.dumps({"pmc_mode": True, "suite": "reference", "variants": [c.op for c in cases]}), flush=True)
-        return 0
     rows, tot_us, tot_flops = {}, 0.0, 0.0
-    for c in cases:
-        fn = lambda f=loaded[c.op]: f(q, k, v)  # noqa: E731
-        w = work(c.op, c.B, c.H, c.S, c.D, {})
-        us = median_us(fn)
-        cu = cold_us(fn, reps=15, flusher=flusher)
-        r = rates(w, us)
-        gs, flex = A100_PUBLISHED_US[c.op]
-        rows[c.op] = {"us": round(us, 2), "cold_us": round(cu, 2), "tflops_alg": round(r["tflops_alg"], 2),
-                      "pct_mfma_peak_alg": round(100 * r["frac_mfma_alg"], 2),
-                      "a100_graphsynth_us": gs, "a100_flex_attention_us": flex}
-        tot_us += us
-        tot_flops += w["flops_alg"]
-        log(f"  ref {c.op:22s} {us:9.1f} us (cold {cu:8.1f})  alg {r['tflops_alg']:7.1f} TF/s "
-            f"({100 * r['frac_mfma_alg']:5.1f}% peak)   A100 GraphSynth {gs} us")
+    for S in seq_lens:
+        cases = reference_suite(S)
+        q, k, v, _ = draw_inputs(cases[0], dev)
+        if args.pmc_mode:  # for rocprofv3 --pmc: each variant twice after a cache flush, nothing timed
+            for c in cases:
+                for _ in range(2):
+                    flusher()
+                    loaded[c.op](q, k, v)
+            torch.cuda.synchronize()
+            continue
+        for c in cases:
+            fn = lambda f=loaded[c.op]: f(q, k, v)  # noqa: E731
+            w = work(c.op, c.B, c.H, c.S, c.D, {})
+            us = median_us(fn)
+            cu = cold_us(fn, reps=15, flusher=flusher)
+            r = rates(w, us)
+            row = {"us": round(us, 2), "cold_us": round(cu, 2), "tflops_alg": round(r["tflops_alg"], 2),
+                   "pct_mfma_peak_alg": round(100 * r["frac_mfma_alg"], 2)}
+            if sweep:
+                a100 = A100_SEQSWEEP_US[c.op][S]
+                row["a100_graphsynth_us"] = a100
+                row["a100_status"] = "generalises" if a100 is not None else "AssertionError"
+                rows.setdefault(c.op, {})[str(S)] = row
+            else:
+                gs, flex = A100_PUBLISHED_US[c.op]
+                row.update(a100_graphsynth_us=gs, a100_flex_attention_us=flex)
+                rows[c.op] = row
+                a100 = gs
+            tot_us += us
+            tot_flops += w["flops_alg"]
+            log(f"  ref {c.op:22s} S{S:5d} {us:9.1f} us (cold {cu:8.1f})  alg {r['tflops_alg']:7.1f} TF/s "
+                f"({100 * r['frac_mfma_alg']:5.1f}% peak)   A100 GraphSynth {a100} us")
+        del q, k, v
+        torch.cuda.empty_cache()
+    if args.pmc_mode:
+        print(json.dumps({"pmc_mode": True, "suite": args.suite, "seq_lens": list(seq_lens)}), flush=True)
+        return 0
+    shape = "B2 H32 S{1024,2048,4096} D128" if sweep else "B2 H32 S2048 D128"
+    src = "results/FINAL_seqsweep.csv:2-31" if sweep else "results/FINAL_flexattention.csv:2-11"
     print(json.dumps({
         "metric": "reference benchmark shape: us/call + algorithmic TFLOP/s per variant", "unit": "us",
-        "higher_is_better": False, "dtype": "bf16", "data": "synthetic (seeded N(0,1), one draw for the ten)",
+        "higher_is_better": False, "dtype": "bf16", "data": "synthetic (seeded N(0,1), one draw per S for the ten)",
         "n_gpus": 1,
         "config": {"workload": "ten variants through <op>_BEST.py::launch_kernel(q, k, v), reference constants, "
-                               "B2 H32 S2048 D128 bf16", "suite": "reference"},
+                               f"{shape} bf16", "suite": args.suite},
         "sum_us": round(tot_us, 2), "tflops_alg_over_sum": round(tot_flops / (tot_us * 1e-6) / 1e12, 2),
         "peak_bf16_tflops": PEAK_BF16_TFLOPS,
-        "a100_context": "results/FINAL_flexattention.csv:2-11 of the reference (A100-SXM4-40GB): context, not a target",
+        "a100_context": f"{src} of the reference (A100-SXM4-40GB): context, not a target",
         "variants": rows,
     }), flush=True)
     return 0
@@ -575,9 +617,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--suite", default="headline", choices=["headline", "northstar", "reference"],
+    ap.add_argument("--suite", default="headline", choices=["headline", "northstar", "reference", "seqsweep"],
                     help="headline: the metric's shape (default); northstar: B4 H16 S4096 D64; reference: the "
-                         "reference's own shape and constants through its loader (own JSON line)")
+                         "reference's own shape and constants through its loader (own JSON line); seqsweep: "
+                         "the same at S = 1024, 2048, 4096, as the reference's sequence sweep")
     ap.add_argument("--no-northstar", action="store_true",
                     help="skip the north-star object (B4 H16 S4096 D64) of the default headline run")
     ap.add_argument("--variants", default="", help="comma-separated subset of variants (profiling runs)")
@@ -624,7 +667,7 @@ def main() -> int:
         return varlen_report(args)
     if args.configs:
         return configs_report(args)
-    if args.suite == "reference":
+    if args.suite in ("reference", "seqsweep"):
         return reference_report(dev, args)
     cases = headline_suite() if args.suite == "headline" else north_star_suite()
     if args.variants:

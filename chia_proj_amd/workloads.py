@@ -5,7 +5,7 @@ unseeded device randn, extra_bench.py:79-81): q, k, v in that order as fp32
 N(0, 1) [B, H, S, D], cast to bf16; per-head temperatures, when a case needs
 them, are drawn after v as 0.5 + 1.5 * U[0, 1).  Configuration k of
 BASELINE.json uses seed 20260000 + k; the headline / north-star / S-sweep
-suites use seed 20261000 + S; the reference-shape suite seed 20262048.
+suites use seed 20261000 + S; the reference-shape suites seed 20260000 + S.
 """
 from __future__ import annotations
 
@@ -87,13 +87,18 @@ def north_star_suite() -> List[Case]:
     return suite(4, 16, 4096, 64, tag="northstar:")
 
 
-def reference_suite() -> List[Case]:
+def reference_suite(S: int = 2048) -> List[Case]:
     """The reference's own benchmark shape and constants: all ten variants at
-    B2 H32 S2048 D128 bf16 with the constants baked into its eager closures
+    B2 H32 S D128 bf16 with the constants baked into its eager closures
     (extra_bench.py:5,32-62; sigmoid_fix.py:34-40) -- window 256, dilation 4,
     block 512, prefix 256, ALiBi slope h+1, temperature 0.5+h/H, softcap 30,
-    causal sigmoid and ReLU.  Seed 20262048 (the reference draws unseeded)."""
-    return [Case(name=f"reference:{op}", op=op, B=2, H=32, S=2048, D=128, seed=20262048) for op in OP_NAMES]
+    causal sigmoid and ReLU.  S = 2048 is its benchmark; its sequence sweep
+    (extra_bench.py:166) adds S = 1024 and 4096 with the same constants.
+    Seed 20260000 + S (20262048 at the benchmark; the reference draws unseeded)."""
+    return [Case(name=f"reference:{op}:S{S}", op=op, B=2, H=32, S=S, D=128, seed=20260000 + S) for op in OP_NAMES]
+
+
+REFERENCE_SWEEP_S = (1024, 2048, 4096)  # extra_bench.py:166
 
 
 def baseline_configs() -> List[Case]:

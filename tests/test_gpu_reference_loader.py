@@ -3,7 +3,9 @@ by glob and loaded with importlib exactly as extra_bench.py:24-27,65-70 does,
 then called as launch_kernel(q, k, v) at the reference's benchmark shape and
 constants (B2 H32 S2048 D128 bf16, extra_bench.py:5,32-62; sigmoid_fix.py:34-40).
 Every (batch, head) slice is gated against the CPU oracle, and the whole output
-against the reference's own statistic (relerr < 3e-2, extra_bench.py:29,121)."""
+against the reference's own statistic (relerr < 3e-2, extra_bench.py:29,121).
+The same modules are then called at the other lengths of the reference's
+sequence sweep, S = 1024 and 4096 (extra_bench.py:166-201)."""
 import glob
 import importlib.util
 import os
@@ -14,7 +16,7 @@ import torch
 
 import oracle
 from chia_proj_amd import gate
-from chia_proj_amd.workloads import draw_inputs, reference_suite
+from chia_proj_amd.workloads import REFERENCE_SWEEP_S, draw_inputs, reference_suite
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -83,3 +85,43 @@ def test_reference_loader_at_reference_shape(case):
             assert res.ok, f"{case.op} b={b} h={h}: {res.status} {res.stats}"
     assert worst_rel < gate.REL_TOL, (case.op, worst_rel)
     _say(f"  {case.op}: {case.B * case.H} slices within the gate, reference relerr {worst_rel:.2e}")
+
+
+_SWEEP_INPUTS = {}
+
+
+@pytest.mark.parametrize("S", [s for s in REFERENCE_SWEEP_S if s != 2048])
+@pytest.mark.parametrize("op", [c.op for c in reference_suite()])
+def test_reference_loader_at_swept_lengths(op, S):
+    """The reference's sequence sweep (extra_bench.py:166-201) calls the same modules
+    at S = 1024 and 4096 with the constants unchanged and keeps a kernel whose output
+    passes relerr < 3e-2 ("generalises").  Every slice is gated at S = 1024; at
+    S = 4096 sixteen (batch, head) slices spread over both batch entries and all heads."""
+    case = next(c for c in reference_suite(S) if c.op == op)
+    _say(f"[loader-sweep] {op} B{case.B} H{case.H} S{S} D{case.D}")
+    (path,) = _discover()[op]
+    launch_kernel = _load(path)
+    if _SWEEP_INPUTS.get("S") != S:
+        _SWEEP_INPUTS.clear()
+        q, k, v, _ = draw_inputs(case, DEV)
+        _SWEEP_INPUTS.update(S=S, qkv=(q, k, v), cpu=(q.cpu(), k.cpu(), v.cpu()))
+    q, k, v = _SWEEP_INPUTS["qkv"]
+    qc, kc, vc = _SWEEP_INPUTS["cpu"]
+    o = launch_kernel(q, k, v)
+    torch.cuda.synchronize()
+    assert o.shape == q.shape and o.dtype == torch.bfloat16
+    assert bool(torch.isfinite(o).all())
+    if S <= 1024:
+        heads = [(b, h) for b in range(case.B) for h in range(case.H)]
+    else:
+        heads = [(b, h) for b in range(case.B) for h in range(b, case.H, 4)]
+    refs = oracle.variant_ref_heads(op, qc, kc, vc, heads)
+    unnorm = op in ("sigmoid_attn", "relu_attn")
+    worst_rel = 0.0
+    for (b, h), ref in zip(heads, refs):
+        out = o[b, h].float().cpu()
+        worst_rel = max(worst_rel, gate.relerr(ref, out))
+        res = gate.north_star_gate(ref, out, scale_aware=unnorm)
+        assert res.ok, f"{op} S={S} b={b} h={h}: {res.status} {res.stats}"
+    assert worst_rel < gate.REL_TOL, (op, S, worst_rel)
+    _say(f"  {op} S{S}: {len(heads)} slices within the gate, reference relerr {worst_rel:.2e}")
