@@ -109,9 +109,9 @@ struct ScoreGrad {
       // u = s c1 (+ sl (j - i)); with softcap t = cap th, th = tanh(u / cap)
       // = 1 - 2 / (1 + 2^(2 u log2e / cap)), and the cap folds into the
       // exponent's fma
-      float t, th = 0.0f, dtdu = 1.0f;
+      float t, th = 0.0f, dtdu = 1.0f, uk = 0.0f;
       if constexpr (SOFTCAP) {
-        const float uk = ALIBI ? __builtin_fmaf(sl, jmi, s * c1) * k2cap : s * c1k2;
+        uk = ALIBI ? __builtin_fmaf(sl, jmi, s * c1) * k2cap : s * c1k2;
         th = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(uk)), 1.0f);
         dtdu = __builtin_fmaf(-th, th, 1.0f);
         t = cap * th;
@@ -129,7 +129,10 @@ struct ScoreGrad {
         dt = dp * p * (1.0f - sg);
       } else {
         p = post * fmaxf(t, 0.0f);
-        dt = t > 0.0f ? dp * post : 0.0f;
+        // [t > 0] = [u > 0], read from u: with softcap, 1 - 2 / (1 + 2^uk)
+        // cancels to exactly 0 for |uk| below about 2^-24, which would drop
+        // the whole derivative of such a score
+        dt = (SOFTCAP ? uk : t) > 0.0f ? dp * post : 0.0f;
       }
       ds = dt * dtdu;
     }

@@ -20,8 +20,8 @@
 //                             + 8 (t >> 2), columns d0 + 8p, hands lane j + 8p
 //                             the four-key groups of dwords 2 wp, 2 wp + 1 of
 //                             column d0 + 8p + j -- the keys of the B operand.
-// The row sum adds the unrounded fp32 weights (D = 128) or, on the matrix
-// core, the e4m3 weights (D = 64 softmax).  Softmax weights are
+// The row sum adds the e4m3 weights that PV uses: decoded back to fp32 on the
+// vector ALU (D = 128) or on the matrix core (D = 64).  Softmax weights are
 // 2^(x - m + 4) with a running max m that moves (rescaling O and l) only when
 // a tile's max exceeds it by more than 4 (log2): weights stay <= 2^8 < 448,
 // the e4m3 maximum, and weights down to 2^-13 of the row max stay normal.
@@ -339,7 +339,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
           else if constexpr (SOFTCAP) arg = __builtin_fmaf(x[kb][e], cA, cB - m_use);
           else arg = x[kb][e] - m_use;
           pw[kb][e] = __builtin_amdgcn_exp2f(arg);
-          if constexpr (!kMfmaSum) l_run += pw[kb][e];
         }
     } else {
       // sigmoid: 2^8 / (1 + 2^(-(t + bias) log2 e)) = rcp(2^-8 e + 2^-8); ReLU: clamp(t, 0, 448)
@@ -370,6 +369,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
       int d = pk_fp8<false>(pw[kb][e0], pw[kb][e0 + 1], 0);
       d = pk_fp8<true>(pw[kb][e0 + 2], pw[kb][e0 + 3], d);
       pb[w] = d;
+    }
+    // D = 128 softmax: the row sum adds the e4m3 weights that PV uses, decoded
+    // from pb, so the rounding of a row's dominant weight cancels in o = PV / l
+    // (with the lazy max that weight is rarely a power of two; summing the fp32
+    // weights instead left up to 2^-4 of it in the numerator alone)
+    if constexpr (NORM == NORM_SOFTMAX && !kMfmaSum) {
+      float ls = 0.f;
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(pb[w], false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(pb[w], true);
+        ls += (lo[0] + lo[1]) + (hi[0] + hi[1]);
+      }
+      l_run += ls;
     }
 
     // O^T += V^T P^T, one MFMA per 32-row d block
