@@ -7,9 +7,10 @@ times its per-tensor descale), so `fp8_ref` is generic.attention_ref on those
 values.  `fp8_emulated` adds the one rounding the FP8 path introduces besides
 its inputs: the attention weights are scaled by 2^8 and rounded to e4m3 (torch's
 float8_e4m3fn cast: round to nearest even), the row sum keeps the unrounded
-weights (the D = 128 kernels do the same; at D = 64 the softmax kernels sum
-the rounded weights on the matrix core, an error of the same order), o is
-rounded to bf16.  It normalises with the exact row max where the
+weights (the kernels sum the rounded ones, so a row's dominant weight, which
+this model keeps exact at 2^8, cancels between PV and the row sum; the
+kernel's error is of the same order or below), o is rounded to bf16.  It
+normalises with the exact row max where the
 kernel uses the running max of the tiles seen so far, so it models the size of
 the rounding error, not its bits; tests gate the kernel at a multiple of the
 emulation's own error against fp8_ref.
