@@ -80,7 +80,12 @@ def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16, reps: int = 5):
     from chia_proj_amd import gate
     from chia_proj_amd.accounting import work
 
-    torch.set_num_threads(max(1, torch.get_num_threads()))
+    # one torch thread per core the process may run on; a host that caps its
+    # share through OMP_NUM_THREADS (the GPU boxes: 16) is held to that cap
+    affinity = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(affinity, cap) if cap > 0 else affinity
+    torch.set_num_threads(threads)
     threads = torch.get_num_threads()
     total_s = 0.0
     total_flops = 0.0
@@ -116,7 +121,8 @@ def cpu_baseline(cases, inputs, outputs, sample_heads: int = 16, reps: int = 5):
         "kind": "port",
         "sample": (f"each variant's reference bf16 eager path (oracle.eager_bf16, extra_bench.py:37-50) on "
                    f"{sample_heads} of the {cases[0].B * cases[0].H} (batch, head) slices, median of {reps} after 1 "
-                   f"warm-up, scaled by B*H/{sample_heads} to the full step; torch CPU threads={threads}"),
+                   f"warm-up, scaled by B*H/{sample_heads} to the full step; torch CPU threads={threads} "
+                   f"(sched_getaffinity: {affinity} cores, OMP_NUM_THREADS cap: {cap or 'none'})"),
         "step_s_scaled": total_s,
         "gate_on_sample": checks,
     }

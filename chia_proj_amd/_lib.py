@@ -17,7 +17,7 @@ NORM_SIGMOID = 1
 NORM_RELU = 2
 NORMS = {"softmax": NORM_SOFTMAX, "sigmoid": NORM_SIGMOID, "relu": NORM_RELU}
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Entry points declared in include/chia_attn.h (checked by the CPU tests).
 EXPORTS = (

@@ -163,7 +163,18 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
   // a row's max is set on its first step and O is rarely rescaled after it.
   constexpr bool kRev = ALIBI && NORM == NORM_SOFTMAX;
   const int n1 = tr1.n_pre + tr1.n2;
+  // A single block's band tiles [a, a + n) are visited in the order
+  // a + ((k - a) mod n): tile T comes at step T mod n in every block that
+  // reads it.  Neighbouring blocks of a window or block mask (equal n, ranges
+  // shifted by BM / BN tiles) then read each shared tile at the same step,
+  // while it is still in L2, rather than BM / BN steps apart.  (Full rows
+  // start at tile 0, where the order is the identity.)
+  const int rot0 = (!kRev && blk1 < 0 && tr0.n_pre == 0 && n0 > 1) ? tr0.start2 % n0 : 0;
+  const int a0 = tr0.start2;
+  // (a separate early return: folded into the tile_at selects below, the
+  // rotation made the compiler keep both TileRange structs in scratch memory)
   auto step_key0 = [&](int s) {
+    if (rot0 != 0 && s < n0) return (a0 + s - rot0 + (s < rot0 ? n0 : 0)) * BN;
     return (s < n0 ? tile_at(tr0, kRev ? n0 - 1 - s : s) : tile_at(tr1, kRev ? n1 - 1 - (s - n0) : s - n0)) * BN;
   };
 
@@ -273,7 +284,8 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
       asm volatile("" ::: "memory");
       if (dma_next < nsteps) issue_step(dma_next++);
       const char* St = lds + (step % NS) * STAGE_BYTES;
-      const int jt0 = tile_at(tr, kRev ? nt - 1 - it : it) * BN;
+      const int jt0 = (pass == 0 && rot0 != 0) ? (a0 + it - rot0 + (it < rot0 ? n0 : 0)) * BN
+                                               : tile_at(tr, kRev ? nt - 1 - it : it) * BN;
 
 #pragma unroll
       for (int kbs = 0; kbs < 2; ++kbs) {

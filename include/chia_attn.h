@@ -29,7 +29,9 @@
 extern "C" {
 #endif
 
-#define CHIA_ATTN_ABI_VERSION 3  /* 2: kv_heads (GQA / MQA); 3: cu_seqlens (packed sequences) */
+#define CHIA_ATTN_ABI_VERSION 4 /* 2: kv_heads (GQA / MQA); 3: cu_seqlens (packed sequences);
+                                   4: chia_attn_bwd_noalloc and status -10, plan units per core
+                                      (block_n is 32 keys on the one-block core, 64 on the paired core) */
 
 /* Normaliser applied to the (modified, masked) scores.
  *   SOFTMAX: p = softmax_j(s) over visible keys   (extra_bench.py:42)

@@ -204,9 +204,10 @@ def test_alibi_softmax_tile_order(name, kw, sign, shape, D):
 def test_softmax_rising_scores(name, kw, shape, D):
     """Scores that rise along the keys: q ~ 4 sqrt(D/64) u, k_j ~ (j / 2) u (u a unit vector)
     plus noise, so a row's max climbs ~23 log2-units per 64-key tile at either head dim.  The
-    softmax weights are first computed against the running reference max and, when a partial row
-    sum over a tile (paired core) or a 32-key step (one-block core) exceeds 2^16, recomputed
-    against the new max; these inputs take that path on almost every tile.  At head dim 64 the
+    paired core first computes a tile's softmax weights against the running reference max and,
+    when a partial row sum over the tile exceeds 2^16, recomputes them against the new max; these
+    inputs take that path on almost every tile.  The one-block core takes the exact row max of
+    every 32-key step, so here they drive its per-step rescale of O and l.  At head dim 64 the
     smaller shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones
     (PAIR, WIDE and WIDE2 steps), and the window / block masks run the one-block core; at head
     dim 128 every case runs the one-block core."""
