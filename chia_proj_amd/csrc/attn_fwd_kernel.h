@@ -629,7 +629,10 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
       for (int st = 0; st < NSTR; ++st) {
         if (masked[qb_of(st)]) {
           // the row's key interval is recomputed here rather than kept live
-          const int i = row0[qb_of(st)] + lq;
+          // (the opaque row index keeps the compiler from hoisting it out of
+          // the tile loop, where the pipelined ReLU kernel spilled it)
+          int i = row0[qb_of(st)] + lq;
+          asm volatile("" : "+v"(i));
           const int jbase = jt0 + 32 * kb_of(st) + 4 * lh;
           const uint32_t hidden = hidden_bits(g, i, jbase);  // bit k: key jbase + k hidden from row i
           // the +-inf pattern in an SGPR (loaded opaquely, so the blend below
