@@ -22,6 +22,7 @@ KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
 KernelFn select_q1_kernel_d64(int norm, bool alibi, bool softcap);
 KernelFn select_kernel_d128(int norm);
 KernelFn select_q1_kernel_d128(int norm, bool alibi, bool softcap);
+KernelFn select_q1_split_kernel_d128(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d128(int norm, bool alibi, bool softcap);
 Fp8KernelFn select_fp8_kernel(int head_dim, int format, int norm, bool alibi, bool softcap);
@@ -106,6 +107,8 @@ struct Geometry {
   int residues;
   int zigzag;
   bool q1;         // the one-block core (attn_fwd_q1_kernel.h)
+  int groups;      // one-block core: groups of `waves` wavefronts per workgroup (2: a
+                   // zigzag pair's steps split between two groups)
   int64_t workgroups;
 };
 
@@ -115,6 +118,7 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
   geo.residues = num_residues(m);
   geo.zigzag = zigzag_of(m) ? 1 : 0;
   geo.q1 = false;
+  geo.groups = 1;
   const int32_t s0 = residue_geom(m, 0).S;  // longest residue class
   // 4 wavefronts share each K/V tile among more rows; fall back to 2 when
   // that leaves fewer than two workgroups per CU.  Windowed or block masks
@@ -161,6 +165,10 @@ Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const Scor
   const int64_t nblk = (s0 + geo.rows - 1) / geo.rows;
   geo.n_pairs = (int)(geo.zigzag ? (nblk + 1) / 2 : nblk);
   geo.workgroups = a->batch * a->heads * geo.residues * geo.n_pairs;
+  // Head dim 128, zigzag pairs on fewer than two workgroups per CU: one group
+  // per workgroup would leave one wavefront per SIMD, so two groups split
+  // each pair's steps (every SIMD then holds two wavefronts).
+  if (a->head_dim == 128 && geo.zigzag && geo.workgroups < 2 * kCUs) geo.groups = 2;
   return geo;
 }
 
@@ -241,12 +249,13 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
 
   KernelFn fn = a->head_dim == 64 ? (geo.q1 ? select_q1_kernel_d64((int)a->norm, sp.alibi, sp.softcap)
                                             : select_kernel_d64(waves, (int)a->norm, sp.alibi, sp.softcap))
-               : geo.q1            ? select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap)
+               : geo.q1            ? (geo.groups == 2 ? select_q1_split_kernel_d128((int)a->norm, sp.alibi, sp.softcap)
+                                                  : select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap))
                                    : select_kernel_d128((int)a->norm);
   if (fn == nullptr) return CHIA_ATTN_ERR_NORM;  // no instantiation for this core and normaliser
   void* kargs[] = {&p};
-  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg), dim3(64 * waves), kargs,
-                                   0, (hipStream_t)stream);
+  hipError_t err = hipLaunchKernel(reinterpret_cast<const void*>(fn), dim3((unsigned)p.n_wg),
+                                   dim3(64 * waves * geo.groups), kargs, 0, (hipStream_t)stream);
   if (err != hipSuccess) return (int)err;
   err = hipGetLastError();
   return err == hipSuccess ? CHIA_ATTN_OK : (int)err;

@@ -51,9 +51,12 @@ struct Q1Config {
   static constexpr int stages = 2;
 };
 
-template <int D, int NORM, bool ALIBI, bool SOFTCAP>
-__global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kernel(const FwdParams p) {
-  constexpr int NW = 4;
+// NG = 2: the workgroup holds two groups of four wavefronts that split one
+// zigzag pair's steps between them (below); NG = 1: one group.
+template <int D, int NORM, bool ALIBI, bool SOFTCAP, int NG = 1>
+__global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_kernel(const FwdParams p) {
+  static_assert(NG == 1 || NG == 2, "one or two groups");
+  constexpr int NW = 4;  // wavefronts per group
   constexpr int BN = kBN;
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;          // rows per block
@@ -74,11 +77,14 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
   constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
   constexpr bool kSigFold = NORM == NORM_SIGMOID && !ALIBI && !SOFTCAP;
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char lds_all[NG * NS * STAGE_BYTES];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_wg = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = NG == 2 ? wave_wg >> 2 : 0;  // this wavefront's group
+  const int wave = wave_wg & (NW - 1);          // and its index in the group
+  char* const lds = lds_all + grp * (NS * STAGE_BYTES);  // the group's LDS stages
   const int lq = lane & 31, lh = lane >> 5;
 
   // ---- workgroup -> (batch, head, residue, unit) ----------------------------
@@ -178,6 +184,25 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
     return (s < n0 ? tile_at(tr0, kRev ? n0 - 1 - s : s) : tile_at(tr1, kRev ? n1 - 1 - (s - n0) : s - n0)) * BN;
   };
 
+  // ---- the group's steps -------------------------------------------------------
+  // NG = 2 (a zigzag pair on a grid of fewer than two workgroups per CU, where
+  // one group alone would leave one wavefront per SIMD): the pair's steps split
+  // at M = ceil(nsteps / 2), group 0 running [0, M) and group 1 [M, nsteps).
+  // Block 1 has at least block 0's steps, so group 0 computes block 0 whole
+  // and block 1's first steps, group 1 the rest of block 1 (of block 0 when
+  // there is no block 1).  The block both groups compute part of is merged at
+  // the end through LDS, with the log-sum-exp rescale of the two partial
+  // (O, m, l).  Each group streams its own tiles through its own LDS stages;
+  // the workgroup barrier of every step is shared, so both groups pass the same
+  // number of barriers: the group with fewer steps adds empty ones.
+  int M = NG == 2 ? (nsteps + 1) / 2 : nsteps;
+  if (NG == 2 && blk1 >= 0 && M < n0) M = n0;  // (not reached for causal pairs)
+  const int s_lo = grp == 1 ? M : 0, s_hi = grp == 1 ? nsteps : M;
+  const int n_bar = imax32(M, nsteps - M);  // step barriers of each group
+  // pass (0: block 0, 1: block 1) that both groups compute part of, or -1
+  const int split_pass =
+      NG == 2 && M > 0 && M < nsteps ? (blk1 >= 0 ? (M > n0 ? 1 : -1) : 0) : -1;
+
   uint32_t k_dma[NDMA], v_dma[NDMA];
 #pragma unroll
   for (int n = 0; n < NDMA; ++n) {
@@ -211,8 +236,8 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
     }
   };
   // prologue: the first NS - 1 steps (each barrier issues one more)
-  int dma_next = 0;
-  for (; dma_next < NS - 1 && dma_next < nsteps; ++dma_next) issue_step(dma_next);
+  int dma_next = s_lo;
+  for (; dma_next < s_lo + NS - 1 && dma_next < s_hi; ++dma_next) issue_step(dma_next);
 
   // per-lane LDS byte offsets (as in attn_fwd_kernel)
   const int k_lane = lq * RP + 16 * k_slot<D>(lq, lh);
@@ -225,12 +250,17 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
   // wavefront runs its exponentials beside them (sigmoid and ReLU measured
   // slower with either)
   constexpr bool kPrio = NORM == NORM_SOFTMAX;
-  int step = 0;
+  int step = s_lo;
+  bool merged = false;
 #pragma unroll 1
   for (int pass = 0; pass < 2; ++pass) {
     const int blk = pass == 0 ? blk0 : blk1;
     if (blk < 0) break;
     const int nt = pass == 0 ? n0 : tr1.n_pre + tr1.n2;
+    // this group's steps of the block: [it_lo, it_hi)
+    const int base = pass == 0 ? 0 : n0;
+    const int it_lo = imax32(s_lo - base, 0), it_hi = imin32(s_hi - base, nt);
+    if (it_lo >= it_hi) continue;
     const TileRange tr = pass == 0 ? tr0 : tr1;
 
     const int row0 = blk * BM + 32 * wave;
@@ -272,7 +302,7 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
     float m_run = -INFINITY, l_run = 0.f;
 
 #pragma unroll 1
-    for (int it = 0; it < nt; ++it, ++step) {
+    for (int it = it_lo; it < it_hi; ++it, ++step) {
       // wait for this step's tile (NS - 2 later steps may stay in flight), then the barrier
       if constexpr (NS >= 3) {
         if (dma_next - (step + 1) >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA) : "memory");
@@ -282,7 +312,7 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
       }
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (dma_next < nsteps) issue_step(dma_next++);
+      if (dma_next < s_hi) issue_step(dma_next++);
       const char* St = lds + (step % NS) * STAGE_BYTES;
       const int jt0 = (pass == 0 && rot0 != 0) ? (a0 + it - rot0 + (it < rot0 ? n0 : 0)) * BN
                                                : tile_at(tr, kRev ? nt - 1 - it : it) * BN;
@@ -442,6 +472,49 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
       }
     }
 
+    // ---- the block both groups computed part of: merge through LDS -------------
+    if constexpr (NG == 2) {
+      if (pass == split_pass) {
+        merged = true;
+        for (int k = s_hi - s_lo; k < n_bar; ++k) __builtin_amdgcn_s_barrier();
+        // every wavefront is past its last step (no DMA in flight, no stage
+        // still read): the stages of both groups hold the merge buffer, per
+        // wavefront of group 1 its 16 DB accumulators, m and l, lane-major
+        constexpr int FL = 16 * DB + 2;
+        float* mb = reinterpret_cast<float*>(lds_all) + wave * (FL * 64) + lane;
+        __syncthreads();
+        if (grp == 1) {
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mb[(16 * db + e) * 64] = oacc[db][e];
+          mb[(16 * DB) * 64] = m_run;
+          mb[(16 * DB + 1) * 64] = l_run;
+        }
+        __syncthreads();
+        if (grp == 1) return;  // group 0 stores the block
+        const float m1 = mb[(16 * DB) * 64], l1 = mb[(16 * DB + 1) * 64];
+        if constexpr (NORM == NORM_SOFTMAX) {
+          // both partials against the larger reference (a row neither group
+          // saw keeps m = -inf, O = 0 and l = 0)
+          const float mm = fmaxf(m_run, m1);
+          const float a0 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
+          const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[db][e] = __builtin_fmaf(oacc[db][e], a0, mb[(16 * db + e) * 64] * a1);
+          l_run = __builtin_fmaf(l_run, a0, l1 * a1);
+          m_run = mm;
+        } else {
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) oacc[db][e] += mb[(16 * db + e) * 64];
+        }
+      }
+    }
+
     // ---- epilogue of this block: normalise and store ---------------------------
     float f;
     if constexpr (NORM == NORM_SOFTMAX) {
@@ -466,6 +539,10 @@ __global__ __launch_bounds__(256, Q1Config<D>::occupancy) void attn_fwd_q1_kerne
           *(u32x2_t*)(dst + 32 * db + 8 * gq) = w;
         }
     }
+  }
+  if constexpr (NG == 2) {
+    if (!merged)
+      for (int k = s_hi - s_lo; k < n_bar; ++k) __builtin_amdgcn_s_barrier();
   }
 }
 

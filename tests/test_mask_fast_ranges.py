@@ -62,3 +62,20 @@ def test_tile_schedule_is_safe(tmp_path):
     planted = subprocess.run([str(exe), "planted"], capture_output=True, text=True)
     assert planted.returncode == 0, planted.stdout + planted.stderr
     assert planted.stdout.count("planted mistake") == 4
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_one_block_split_schedule_is_safe(tmp_path):
+    """The one-block core with two groups per workgroup (a zigzag pair's steps split
+    between them, the shared block merged through LDS): every step computed once,
+    equal barrier counts and roles in both groups, each group's two-stage DMA safe,
+    the merge buffer inside the LDS; and each of four planted mistakes is caught."""
+    exe = tmp_path / "check_q1_split"
+    subprocess.run(["g++", "-std=c++17", "-O1", *SANITIZE, f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+                    str(ROOT / "tests" / "cpp" / "check_q1_split.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "0 violations" in out.stdout
+    planted = subprocess.run([str(exe), "planted"], capture_output=True, text=True)
+    assert planted.returncode == 0, planted.stdout + planted.stderr
+    assert planted.stdout.count("planted mistake") == 4
