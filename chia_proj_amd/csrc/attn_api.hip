@@ -478,7 +478,12 @@ extern "C" int chia_attn_fwd_fp8(const chia_attn_fp8_args* fa, void* stream) {
   p.H = (int32_t)a->heads;
   p.residues = num_residues(p.mask);
   p.n_blk = (residue_geom(p.mask, 0).S + 127) / 128;
-  const int64_t n_wg = a->batch * a->heads * p.residues * (int64_t)p.n_blk;
+  const int64_t bhr = a->batch * a->heads * p.residues;
+  const int64_t n_wg = bhr * (int64_t)p.n_blk;
+  // Causal rows without a window: a block's work grows with its index, and the
+  // launch walks the longest blocks of every slice first (per XCD).
+  if (zigzag_of(p.mask) && !a->cu_seqlens && bhr % 8 == 0) p.rank_hx = (int32_t)(bhr / 8);
+  p.div_hx = make_udiv(p.rank_hx > 0 ? p.rank_hx : 1);
   if (n_wg >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
   p.n_wg = (int32_t)n_wg;
   p.div_blk = make_udiv(p.n_blk);

@@ -68,6 +68,10 @@ struct Fp8Params {
   // seq_order[i] is the sequence of batch slot i (longest first).
   const int32_t* cu_seqlens;
   const int32_t* seq_order;
+  // Longest-first launch order for causal rows (fixed length, B H residues a
+  // multiple of 8): the (b, h, residue) slices per XCD, 0 otherwise; and its divider.
+  int32_t rank_hx;
+  UDiv div_hx;
 };
 
 // Swizzled 16-byte slot of chunk c of row r in an fp8 tile of D-byte rows.
@@ -120,10 +124,23 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   const int lq = lane & 31, lh = lane >> 5;
 
   // workgroup -> (b, h, residue, 128-row block), the blocks with the most keys
-  // first; packed sequences go round-robin to the XCDs (no contiguous ranges)
-  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = udiv(L, p.div_blk);
-  const int blk = p.n_blk - 1 - (L - bhr * p.n_blk);
+  // first.  Causal rows (rank_hx > 0): XCD x (workgroups x, x + 8, ...) serves
+  // slices [x rank_hx, (x + 1) rank_hx) and walks them rank by rank, every
+  // slice's last block, then every slice's second to last, ..., so the longest
+  // blocks all start first and the shortest fill the end of the launch.
+  // Otherwise each XCD gets a contiguous range of slices, longest block first
+  // per slice; packed sequences go round-robin to the XCDs.
+  int bhr, blk;
+  if (p.rank_hx > 0) {
+    const int xcd = (int)(blockIdx.x & 7), local = (int)(blockIdx.x >> 3);
+    const int rank = udiv(local, p.div_hx);
+    bhr = xcd * p.rank_hx + (local - rank * p.rank_hx);
+    blk = p.n_blk - 1 - rank;
+  } else {
+    const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
+    bhr = udiv(L, p.div_blk);
+    blk = p.n_blk - 1 - (L - bhr * p.n_blk);
+  }
   const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
   const int bs = udiv(bh, p.div_h), h = bh - bs * p.H;
   const int b = seq_of(p.seq_order, bs);
