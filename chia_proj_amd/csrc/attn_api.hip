@@ -109,6 +109,7 @@ struct Geometry {
   bool q1;         // the one-block core (attn_fwd_q1_kernel.h)
   int groups;      // one-block core: groups of `waves` wavefronts per workgroup (2: a
                    // zigzag pair's steps split between two groups)
+  bool rank;       // launch the units with the most keys first (rank_order)
   int64_t workgroups;
 };
 
@@ -119,6 +120,7 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
   geo.zigzag = zigzag_of(m) ? 1 : 0;
   geo.q1 = false;
   geo.groups = 1;
+  geo.rank = false;
   const int32_t s0 = residue_geom(m, 0).S;  // longest residue class
   // 4 wavefronts share each K/V tile among more rows; fall back to 2 when
   // that leaves fewer than two workgroups per CU.  Windowed or block masks
@@ -155,13 +157,26 @@ Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const Scor
   Geometry geo = paired_geometry(m, a->batch, a->heads);
   const bool banded = m.hi < kInf || m.blk > 0;
   const int32_t s0 = residue_geom(m, 0).S;
-  if (a->head_dim == 64 && !banded) return geo;
+  // Causal rows with a prefix every query sees: a row block's work is the
+  // prefix or its causal band, whichever is longer, which zigzag pairs do not
+  // balance.  At head dim 64 such rows run the one-block core, one block per
+  // workgroup, the blocks with the most keys launched first (prefix-LM 1024,
+  // B4 H16 D64: 173.3 -> 164.0 us at S4096, 62.6 -> 56.9 us at S2048; the same
+  // order on the paired core, 166.0 / 62.3 us).  Plain causal rows keep the
+  // zigzag pairs: the one-block core launched longest-first measured within
+  // 3 % of them (temperature 156.8 -> 159.3 us, softcap 217.5 -> 211.9 us).
+  const bool prefix_causal = geo.zigzag && m.prefix > 0;
+  if (a->head_dim == 64 && !banded && !prefix_causal) return geo;
   if (a->head_dim == 128 && a->norm != CHIA_ATTN_NORM_SOFTMAX && !geo.zigzag && !banded && s0 >= 2048 && !sp.alibi &&
       !sp.softcap && geo.waves == 4)
     return geo;
   geo.q1 = true;
   geo.waves = 4;
   geo.rows = 128;
+  if (a->head_dim == 64 && prefix_causal) {
+    geo.zigzag = 0;
+    geo.rank = true;
+  }
   const int64_t nblk = (s0 + geo.rows - 1) / geo.rows;
   geo.n_pairs = (int)(geo.zigzag ? (nblk + 1) / 2 : nblk);
   geo.workgroups = a->batch * a->heads * geo.residues * geo.n_pairs;
@@ -237,6 +252,9 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   const int waves = geo.waves;
   if (geo.workgroups >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
   p.n_wg = (int32_t)geo.workgroups;
+  const int64_t slices = a->batch * a->heads * p.residues;
+  if (geo.rank && !a->cu_seqlens && slices % 8 == 0) p.rank_hx = (int32_t)(slices / 8);
+  p.div_hx = make_udiv(p.rank_hx > 0 ? p.rank_hx : 1);
   p.div_pairs = make_udiv(p.n_pairs);
   p.div_res = make_udiv(p.residues);
   p.div_h = make_udiv(p.H);

@@ -111,7 +111,26 @@ struct FwdParams {
   const int32_t* cu_seqlens;       // packed sequences: [B + 1] token offsets, or nullptr
   const int32_t* seq_order;        // packed sequences: dispatch order of the B sequences, or nullptr
   float scale, softcap, bias, post_scale;
+  // Longest-first launch order (rows whose work grows with the block index;
+  // fixed length, B H residues a multiple of 8): the (b, h, residue) slices
+  // per XCD, 0 otherwise; and its divider.  See rank_order().
+  int32_t rank_hx;
+  UDiv div_hx;
 };
+
+// Workgroup -> (slice, unit) in the longest-first order: XCD x (workgroups x,
+// x + 8, ...) serves slices [x hx, (x + 1) hx) and walks them rank by rank,
+// every slice's last unit, then every slice's second to last, ..., so the
+// units with the most keys all start first and the shortest fill the end of
+// the launch.  Bijective when the launch has 8 hx n_units workgroups.
+struct SliceUnit {
+  int slice, unit;
+};
+__device__ __forceinline__ SliceUnit rank_order(int x, int hx, UDiv div_hx, int n_units) {
+  const int xcd = x & 7, local = x >> 3;
+  const int rank = udiv(local, div_hx);
+  return SliceUnit{xcd * hx + (local - rank * hx), n_units - 1 - rank};
+}
 
 // Packed sequences: sequence b's first token and length (at most the launch's
 // S); fixed-length batches: 0 and S.
@@ -274,9 +293,16 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // ---- workgroup -> (batch, head, residue, row-block pair) -----------------
   // Packed sequences of unequal length: consecutive workgroups go round-robin
   // to the XCDs so every XCD gets a share of every sequence's work.
-  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = udiv(L, p.div_pairs);
-  const int pr = L - bhr * p.n_pairs;
+  int bhr, pr;
+  if (p.rank_hx > 0) {
+    const SliceUnit su = rank_order((int)blockIdx.x, p.rank_hx, p.div_hx, p.n_pairs);
+    bhr = su.slice;
+    pr = su.unit;
+  } else {
+    const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
+    bhr = udiv(L, p.div_pairs);
+    pr = L - bhr * p.n_pairs;
+  }
   const int bh = udiv(bhr, p.div_res);
   const int r = bhr - bh * p.residues;
   const int bs = udiv(bh, p.div_h);

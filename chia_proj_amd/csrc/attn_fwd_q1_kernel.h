@@ -88,9 +88,16 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
   const int lq = lane & 31, lh = lane >> 5;
 
   // ---- workgroup -> (batch, head, residue, unit) ----------------------------
-  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = udiv(L, p.div_pairs);
-  const int pr = L - bhr * p.n_pairs;
+  int bhr, pr;
+  if (p.rank_hx > 0) {
+    const SliceUnit su = rank_order((int)blockIdx.x, p.rank_hx, p.div_hx, p.n_pairs);
+    bhr = su.slice;
+    pr = su.unit;
+  } else {
+    const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
+    bhr = udiv(L, p.div_pairs);
+    pr = L - bhr * p.n_pairs;
+  }
   const int bh = udiv(bhr, p.div_res);
   const int r = bhr - bh * p.residues;
   const int bs = udiv(bh, p.div_h);

@@ -162,16 +162,18 @@ def test_plan_geometry(lib_built):
     # causal without a window pairs row blocks (i, n-1-i); every pair is one workgroup
     p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, causal=True))
     assert p["waves"] == 4 and p["block_m"] == 256 and p["workgroups"] == 4 * 16 * 8
-    # a window or block mask runs the one-block core: 128-row blocks, one per
-    # workgroup, 32-key steps
-    for kw in (dict(causal=True, window=256), dict(causal=False, block=256), dict(causal=True, window=129)):
+    # a window or block mask, or causal rows with a prefix (whose block work
+    # zigzag pairs do not balance), runs the one-block core: 128-row blocks,
+    # one per workgroup, 32-key steps
+    for kw in (dict(causal=True, window=256), dict(causal=False, block=256), dict(causal=True, window=129),
+               dict(causal=True, prefix=1024)):
         p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, **kw))
         assert (p["waves"], p["block_m"], p["block_n"], p["workgroups"]) == (4, 128, 32, 4 * 16 * 16)
     # every visible pair is inside a computed 32 x block_n step
     for kw in (dict(causal=True), dict(causal=True, window=256), dict(causal=False, block=256),
                dict(causal=True, dilation=2, window=1024), dict(causal=True, prefix=1024)):
         p = _lib.plan(make_args(batch=1, heads=1, seqlen=4096, head_dim=64, **kw))
-        assert p["block_n"] == (32 if ("window" in kw or "block" in kw) else 64)
+        assert p["block_n"] == (32 if ("window" in kw or "block" in kw or "prefix" in kw) else 64)
         assert p["wave_tiles_visited"] * 32 * p["block_n"] >= p["pairs_visible"]
         assert p["wave_tiles_partial"] <= p["wave_tiles_visited"]
 
