@@ -455,8 +455,17 @@ int launch_bwd(const chia_attn_bwd_args* ba, void* stream, bool noalloc) {
                                           : select_bwd_kernels_d128((int)a->norm, alibi, softcap);
   const hipStream_t s = (hipStream_t)stream;
   hipError_t err = hipSuccess;
+  // Causal rows: each kernel launches its blocks with the most work first
+  // (rank_order): the last query blocks (dQ), the first key blocks (dK/dV).
+  auto rank_for = [&](int64_t slices) {
+    const bool on = zigzag_of(p.mask) && !a->cu_seqlens && slices % 8 == 0;
+    p.rank_hx = on ? (int32_t)(slices / 8) : 0;
+    p.div_hx = make_udiv(on ? p.rank_hx : 1);
+  };
   if (softmax) err = launch(ks.stats, g_stats, p, s);
+  rank_for(a->batch * a->heads * p.residues);
   if (err == hipSuccess) err = launch(ks.dq, g_dq, p, s);
+  rank_for(a->batch * hkv * p.residues);
   if (err == hipSuccess) err = launch(ks.dkdv, g_dkdv, p, s);
   return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
 }

@@ -75,6 +75,10 @@ struct BwdParams {
   int32_t n_blk, n_wg;  // 128-row (or key) blocks per (b, head, residue 0); grid
   UDiv div_blk, div_res, div_h, div_g, div_hk, div_dil;
   float scale, softcap, bias, post_scale;
+  // Causal rows: the launched kernel's slices per XCD for the longest-first
+  // order (rank_order), 0 otherwise; and its divider.
+  int32_t rank_hx;
+  UDiv div_hx;
 };
 
 // Per-score gradient (see the header): from the raw s = q.k, dp = do.v and
@@ -248,9 +252,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
 
   // workgroup -> (b, h, residue, 128-row block), heaviest blocks first
   // (packed sequences of unequal length: round-robin over the XCDs, no remap)
-  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = udiv(L, p.div_blk);
-  const int blk = p.n_blk - 1 - (L - bhr * p.n_blk);
+  // the query blocks with the most keys first
+  int bhr, blk;
+  if (p.rank_hx > 0) {
+    const SliceUnit su = rank_order((int)blockIdx.x, p.rank_hx, p.div_hx, p.n_blk);
+    bhr = su.slice;
+    blk = su.unit;
+  } else {
+    const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
+    bhr = udiv(L, p.div_blk);
+    blk = p.n_blk - 1 - (L - bhr * p.n_blk);
+  }
   const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
   const int bs = udiv(bh, p.div_h), h = bh - bs * p.H;
   const int b = seq_of(p.seq_order, bs);
@@ -421,9 +433,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
   // workgroup -> (b, K/V head, residue, 128-key block); low blocks (seen by
   // the most rows under a causal mask) first
   const int HK = p.H / p.G;
-  const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
-  const int bhr = udiv(L, p.div_blk);
-  const int blk = L - bhr * p.n_blk;
+  // the key blocks with the most queries (the first ones) first
+  int bhr, blk;
+  if (p.rank_hx > 0) {
+    const SliceUnit su = rank_order((int)blockIdx.x, p.rank_hx, p.div_hx, p.n_blk);
+    bhr = su.slice;
+    blk = p.n_blk - 1 - su.unit;
+  } else {
+    const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
+    bhr = udiv(L, p.div_blk);
+    blk = L - bhr * p.n_blk;
+  }
   const int bh = udiv(bhr, p.div_res), r = bhr - bh * p.residues;
   const int bs = udiv(bh, p.div_hk), hkv = bh - bs * HK;
   const int b = seq_of(p.seq_order, bs);
