@@ -26,8 +26,8 @@
 // a tile's max exceeds it by more than 4 (log2): weights stay <= 2^8 < 448,
 // the e4m3 maximum, and weights down to 2^-13 of the row max stay normal.
 // Sigmoid weights are scaled by 2^8; ReLU weights are clamped to 448.  One workgroup = 4 wavefronts x 32 query rows; K and V tiles of 64 keys
-// are DMA'd HBM -> LDS (16-byte chunks XOR-swizzled by row) in three stages
-// with one barrier per tile, as in the bf16 kernels.
+// are DMA'd HBM -> LDS (16-byte chunks XOR-swizzled by row) in four stages at
+// head dim 64 (three at 128) with one barrier per tile, as in the bf16 kernels.
 #pragma once
 #include "attn_bwd_kernel.h"  // attn_fwd_kernel.h and zero_hidden
 
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   constexpr int RP = D;                 // LDS row pitch (bytes)
   constexpr int T_BYTES = BN * RP;
   constexpr int STAGE_BYTES = 2 * T_BYTES;
-  constexpr int NS = 3;
+  constexpr int NS = D == 64 ? 4 : 3;  // LDS stages (head dim 64: 32 KB, still four workgroups per CU)
   constexpr int KC = D / 64;            // 64-deep steps of the QK^T MFMA
   constexpr int DB = D / 32;            // 32-row d blocks of O^T
   constexpr int NDMA2 = 2 * (BN * (D / 16) / 256);  // DMA loads per tile per wavefront (K and V)
@@ -132,10 +132,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   // per slice; packed sequences go round-robin to the XCDs.
   int bhr, blk;
   if (p.rank_hx > 0) {
-    const int xcd = (int)(blockIdx.x & 7), local = (int)(blockIdx.x >> 3);
-    const int rank = udiv(local, p.div_hx);
-    bhr = xcd * p.rank_hx + (local - rank * p.rank_hx);
-    blk = p.n_blk - 1 - rank;
+    const SliceUnit su = rank_order((int)blockIdx.x, p.rank_hx, p.div_hx, p.n_blk);
+    bhr = su.slice;
+    blk = su.unit;
   } else {
     const int L = p.cu_seqlens ? (int)blockIdx.x : xcd_remap(blockIdx.x, p.n_wg);
     bhr = udiv(L, p.div_blk);
@@ -224,8 +223,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
 
   for (int it = 0; it < ntiles; ++it) {
-    if (dma_next - (it + 1) >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA2) : "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // this tile has landed; the loads of up to NS - 2 later tiles may stay in flight
+    {
+      const int inflight = dma_next - (it + 1);
+      if (NS >= 4 && inflight >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NDMA2) : "memory");
+      else if (inflight >= 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NDMA2) : "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (dma_next < ntiles) issue(dma_next++);
