@@ -339,6 +339,12 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64));  // loads per tile per wavefront
   int dma_next = 0;
   for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+  // Q, dO and the row statistics in registers before the loop: otherwise the
+  // compiler's waits for these loads sink into the loop, where their vmcnt
+  // also drains the K/V tiles in flight (the compiler does not count the DMA)
+#pragma unroll
+  for (int kk = 0; kk < DK; ++kk) asm volatile("" : "+v"(qf[kk]), "+v"(df[kk]));
+  asm volatile("" : "+v"(lse2), "+v"(delta));
 
   typedef short i16x8_t __attribute__((ext_vector_type(8)));
   for (int it = 0; it < ntiles; ++it) {
@@ -549,6 +555,9 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
   constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64)) + (kStats ? 1 : 0);
   int dma_next = 0;
   for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+  // K and V in registers before the loop (see the dQ kernel)
+#pragma unroll
+  for (int kk = 0; kk < DK; ++kk) asm volatile("" : "+v"(kf[kk]), "+v"(vf[kk]));
 
   typedef short i16x8_t __attribute__((ext_vector_type(8)));
   for (int it = 0; it < ntiles; ++it) {

@@ -221,6 +221,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   };
   int dma_next = 0;
   for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+  // Q in registers before the loop: otherwise the compiler's wait for these
+  // loads sinks into the loop as vmcnt(0), which also drains the K/V tiles in
+  // flight on every tile (the compiler does not count the DMA)
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) asm volatile("" : "+v"(qf[kc]));
 
   for (int it = 0; it < ntiles; ++it) {
     // this tile has landed; the loads of up to NS - 2 later tiles may stay in flight
