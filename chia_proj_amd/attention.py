@@ -293,6 +293,41 @@ def _op_forward(q, k, v, params):
 
 def run_backward(do, q, k, v, o, lse, params):
     """dq, dk, dv by chia_attn_bwd (lse: the forward's float32 [B, H, S], softmax only)."""
+    # Fast path, as attention()'s: a call with the shapes, layouts and parameters
+    # of an earlier one (per-head values arrive as float32 device vectors) reuses
+    # its validated argument structs; only the data pointers are new.
+    hs_in, sl_in = params["head_scale"], params["alibi_slopes"]
+    try:
+        key = ("bwd", q.shape, q.dtype, q.device, q.stride(), k.shape, k.dtype, k.stride(), v.shape, v.dtype,
+               v.stride(), o.shape, o.dtype, o.stride(), do.shape, do.dtype, do.stride(), lse is None,
+               params["norm"], params["causal"], params["window"], params["dilation"], params["block"],
+               params["prefix"], params["scale"], params["softcap"], params["bias"], params["post_scale"],
+               tuple(None if t is None else (tuple(t.shape), t.device) for t in (hs_in, sl_in)))
+        # device vectors the full path would pass through unchanged (float32, contiguous)
+        if not all(t is None or (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float32
+                                 and t.is_contiguous()) for t in (hs_in, sl_in)):
+            key = None
+    except (AttributeError, TypeError):
+        key = None
+    cache = _args_cache()
+    entry = cache.get(key) if key is not None else None
+    if entry is not None:
+        b, nbytes = entry
+        a = b.fwd.contents
+        ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), do.data_ptr())
+        if not (ptrs[0] | ptrs[1] | ptrs[2] | ptrs[3] | ptrs[4]) & 15:
+            dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+            a.q, a.k, a.v, a.o = ptrs[:4]
+            a.head_scale = hs_in.data_ptr() if hs_in is not None else None
+            a.alibi_slopes = sl_in.data_ptr() if sl_in is not None else None
+            b.dout, b.dq, b.dk, b.dv = ptrs[4], dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+            b.lse = lse.data_ptr() if lse is not None else None
+            b.workspace = ws.data_ptr()
+            _lib.bwd(b, _current_stream(q))
+            del ws  # queued: any reuse of its memory is ordered after the launch
+            return dq, dk, dv
+
     # q_, k_, v_ (layout copies where needed) and the per-head vectors hs, sl stay
     # referenced until the launch is queued: do_, dq, dk, dv and the workspace are
     # allocated below and must not take their memory.
@@ -314,6 +349,15 @@ def run_backward(do, q, k, v, o, lse, params):
         st[0], st[1], st[2] = _strides3(t)
     with torch.cuda.device(q_.device):
         _lib.bwd(b, torch.cuda.current_stream(q_.device).cuda_stream)
+    # Cache the validated call when no tensor needed a layout change and the
+    # gradients would get the strides of fresh empty_like tensors.
+    if (key is not None and q_ is q and k_ is k and v_ is v and do_ is do
+            and (dq.stride(), dk.stride(), dv.stride()) == (torch.empty_like(q).stride(),
+                                                            torch.empty_like(k).stride(),
+                                                            torch.empty_like(v).stride())):
+        cache[key] = (b, nbytes)
+        if len(cache) > _ARGS_CACHE_MAX:
+            cache.popitem(last=False)
     del q_, k_, v_, hs, sl, ws  # queued: any reuse of their memory is ordered after the launch
     return dq, dk, dv
 

@@ -103,7 +103,17 @@ def _backward(ctx, do, _dlse):
     q, k, v, o, lse = ctx.saved_tensors
     if do is None:
         return (None,) * (3 + len(ctx.rest))
-    dq, dk, dv = torch.ops.chia_attn.bwd(do, q, k, v, o, lse, *ctx.rest)
+    # traced (torch.compile, make_fx / AOTAutograd: a dispatch mode is active, or
+    # fake / meta tensors): the registered operator, one node of the graph;
+    # eager on the GPU: the same implementation without a second operator dispatch
+    traced = (torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack() > 0
+              or type(do) is not torch.Tensor or do.device.type != "cuda")
+    if traced:
+        dq, dk, dv = torch.ops.chia_attn.bwd(do, q, k, v, o, lse, *ctx.rest)
+    else:
+        from .attention import run_backward
+
+        dq, dk, dv = run_backward(do, q, k, v, o, lse if lse.numel() else None, _params(*ctx.rest))
     return (dq, dk, dv) + (None,) * len(ctx.rest)
 
 
