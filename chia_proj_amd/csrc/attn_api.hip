@@ -444,17 +444,16 @@ int launch_bwd(const chia_attn_bwd_args* ba, void* stream, bool noalloc) {
   p.bias = a->bias;
   p.post_scale = a->post_scale;
 
-  const int64_t rows = a->batch * a->heads * a->seqlen;
-  const int64_t g_stats = (rows + 255) / 256;
   const int64_t g_dq = a->batch * a->heads * p.residues * (int64_t)p.n_blk;
   const int64_t g_dkdv = a->batch * hkv * p.residues * (int64_t)p.n_blk;
-  if (g_stats >= ((int64_t)1 << 31) || g_dq >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
+  if (g_dq >= ((int64_t)1 << 31)) return CHIA_ATTN_ERR_SHAPE;
 
   const bool alibi = a->alibi_slopes != nullptr, softcap = a->softcap > 0.f;
   const BwdKernels ks = a->head_dim == 64 ? select_bwd_kernels_d64((int)a->norm, alibi, softcap)
                                           : select_bwd_kernels_d128((int)a->norm, alibi, softcap);
   const hipStream_t s = (hipStream_t)stream;
   hipError_t err = hipSuccess;
+  // dQ first: with softmax it also writes the row statistics dK/dV reads.
   // Causal rows: each kernel launches its blocks with the most work first
   // (rank_order): the last query blocks (dQ), the first key blocks (dK/dV).
   auto rank_for = [&](int64_t slices) {
@@ -462,11 +461,12 @@ int launch_bwd(const chia_attn_bwd_args* ba, void* stream, bool noalloc) {
     p.rank_hx = on ? (int32_t)(slices / 8) : 0;
     p.div_hx = make_udiv(on ? p.rank_hx : 1);
   };
-  if (softmax) err = launch(ks.stats, g_stats, p, s);
   rank_for(a->batch * a->heads * p.residues);
-  if (err == hipSuccess) err = launch(ks.dq, g_dq, p, s);
+  err = launch(ks.dq, g_dq, p, s);
   rank_for(a->batch * hkv * p.residues);
-  if (err == hipSuccess) err = launch(ks.dkdv, g_dkdv, p, s);
+  // a group whose query heads differ in scale takes c1 per score
+  const BwdKernelFn dkdv = G > 1 && a->head_scale ? ks.dkdv_head_c1 : ks.dkdv;
+  if (err == hipSuccess) err = launch(dkdv, g_dkdv, p, s);
   return err == hipSuccess ? CHIA_ATTN_OK : (int)err;
 }
 }  // namespace

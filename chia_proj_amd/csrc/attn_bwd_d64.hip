@@ -1,13 +1,13 @@
 // attn_bwd_d64.hip -- instantiations of the backward kernels for head_dim 64:
-// 3 normalisers x ALiBi on/off x softcap on/off.
+// 3 normalisers x ALiBi on/off x softcap on/off (dK/dV also with per-head c1).
 #include "attn_bwd_kernel.h"
 
 namespace chia {
 
 template <int NORM, bool AL, bool SC>
 static BwdKernels bwd_inst() {
-  return BwdKernels{attn_bwd_stats_kernel<64>, attn_bwd_dq_kernel<64, NORM, AL, SC>,
-                    attn_bwd_dkdv_kernel<64, NORM, AL, SC>};
+  return BwdKernels{attn_bwd_dq_kernel<64, NORM, AL, SC>, attn_bwd_dkdv_kernel<64, NORM, AL, SC, false>,
+                    attn_bwd_dkdv_kernel<64, NORM, AL, SC, true>};
 }
 
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap) {

@@ -13,13 +13,14 @@
 // Masked pairs have p = ds = 0.  The reference is forward-only; this follows
 // the textbook derivation (autograd of the same formula is the oracle).
 //
-// Three launches, no atomics:
-//   * attn_bwd_stats_kernel: per row, lse log2 e and delta, into a workspace
-//     laid out per dilation residue (contiguous rows for the two kernels);
+// Two launches, no atomics:
 //   * attn_bwd_dq_kernel: a workgroup owns 128 query rows (32 per wavefront)
 //     and streams the K / V tiles of their key range -- the forward's layout:
 //     S^T = K Q^T and dP^T = V dO^T with Q, dO in registers, dS^T from the
-//     lane's row statistics, dQ^T += K^T dS^T with K read transposed;
+//     lane's row statistics, dQ^T += K^T dS^T with K read transposed.  With
+//     softmax it first computes its rows' statistics (lse log2 e and
+//     delta = do . o) and stores them, negated delta, into a workspace laid
+//     out per dilation residue (contiguous rows) for the second kernel;
 //   * attn_bwd_dkdv_kernel: a workgroup owns 128 keys (32 per wavefront) of
 //     one K/V head and streams the Q / dO tiles of the rows that see them, for
 //     every query head of the group (GQA): S = Q K^T and dP = dO V^T with K, V
@@ -66,7 +67,7 @@ struct BwdParams {
   int64_t lse_sb, lse_sh, lse_ss;
   const int32_t* cu_seqlens;  // packed sequences: [B + 1] token offsets, or nullptr
   const int32_t* seq_order;   // packed sequences: dispatch order of the B sequences, or nullptr
-  float* stats;         // softmax: [B, H, R, SR] lse log2 e, then [B, H, R, SR] delta
+  float* stats;         // softmax: [B, H, R, SR] lse log2 e, then [B, H, R, SR] -delta
   const float* head_scale;
   const float* alibi_slopes;
   MaskSpec mask;
@@ -82,10 +83,9 @@ struct BwdParams {
 };
 
 // Per-score gradient (see the header): from the raw s = q.k, dp = do.v and
-// j - i, the probability p (for dV) and ds (for dQ, dK).  Softmax: delta is
-// the row statistic delta c1, so ds = p (dp c1 - delta c1) includes c1; sigmoid
-// / ReLU: ds / c1, and the caller applies c1 (once per accumulated gradient
-// where it is uniform).
+// j - i, the probability p (for dV) and ds / c1 (for dQ, dK); the caller
+// applies c1, once per accumulated gradient where it is uniform.  Softmax: the
+// dP accumulator starts from -delta_i, so `dp` here is already dp - delta.
 template <int NORM, bool ALIBI, bool SOFTCAP>
 struct ScoreGrad {
   float c1, c1l2, sl, cap, k2cap, post, nbias_l2;
@@ -93,13 +93,12 @@ struct ScoreGrad {
   float c1k2;   // c1 * k2cap
   float capl2;  // cap * log2 e
 
-  __device__ __forceinline__ void operator()(float s, float dp, float jmi, float lse2, float delta, float& p,
-                                             float& ds) const {
+  __device__ __forceinline__ void operator()(float s, float dp, float jmi, float lse2, float& p, float& ds) const {
     if constexpr (!ALIBI && !SOFTCAP) {
       // t = s c1: the scale folds into one fma ahead of the exponential
       if constexpr (NORM == NORM_SOFTMAX) {
         p = __builtin_amdgcn_exp2f(__builtin_fmaf(s, c1l2, -lse2));
-        ds = p * __builtin_fmaf(dp, c1, -delta);  // delta: the row's delta c1
+        ds = p * dp;
       } else if constexpr (NORM == NORM_SIGMOID) {
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(__builtin_fmaf(s, -c1l2, nbias_l2)));
         p = post * sg;
@@ -125,7 +124,7 @@ struct ScoreGrad {
       float dt;
       if constexpr (NORM == NORM_SOFTMAX) {
         p = __builtin_amdgcn_exp2f(SOFTCAP ? __builtin_fmaf(th, capl2, -lse2) : __builtin_fmaf(t, kLog2e, -lse2));
-        dt = p * __builtin_fmaf(dp, c1, -delta);
+        dt = p * dp;
       } else if constexpr (NORM == NORM_SIGMOID) {
         const float z = SOFTCAP ? __builtin_fmaf(-th, capl2, nbias_l2) : __builtin_fmaf(-t, kLog2e, nbias_l2);
         const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z));
@@ -200,43 +199,26 @@ __device__ __forceinline__ void dma_rows(const uint16_t* base, int64_t rs, int r
 // Kernel set of one (head_dim, normaliser, ALiBi, softcap) instantiation.
 using BwdKernelFn = void (*)(BwdParams);
 struct BwdKernels {
-  BwdKernelFn stats, dq, dkdv;
+  BwdKernelFn dq, dkdv, dkdv_head_c1;  // dkdv_head_c1: a group's heads differ in scale
 };
 
-// ---- row statistics ----------------------------------------------------------
-// One thread per (b, h, row): lse log2 e and delta = do . o, stored at
-// [b, h, residue, row / dil] so each residue's rows are contiguous.
-template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_stats_kernel(const BwdParams p) {
-  const int S = p.mask.S;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= (int64_t)p.B * p.H * S) return;
-  const int bh = (int)(idx / S);
-  const int i = (int)(idx - (int64_t)bh * S);
-  const int b = udiv(bh, p.div_h), h = bh - b * p.H;
-  const SeqSpan seq = seq_span(p.cu_seqlens, b, S);
-  if (i >= seq.len) return;
-  const int64_t t = seq.tok0 + i;
-  const uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + t * p.o_ss;
-  const uint16_t* drow = p.dout + b * p.do_sb + h * p.do_sh + t * p.do_ss;
+// do . o over the 8 DK bf16 values of one lane's half row (chunks 16 kk + 8 lh
+// of the dQ kernel's register layout), in fp32.
+template <int DK>
+__device__ __forceinline__ float half_row_dot(const bf16x8_t* x, const bf16x8_t* y) {
   float acc = 0.f;
 #pragma unroll
-  for (int c = 0; c < D / 8; ++c) {
-    const u32x4_t ov = *(const u32x4_t*)(orow + 8 * c);
-    const u32x4_t dv = *(const u32x4_t*)(drow + 8 * c);
+  for (int kk = 0; kk < DK; ++kk) {
+    const u32x4_t a = __builtin_bit_cast(u32x4_t, x[kk]), b = __builtin_bit_cast(u32x4_t, y[kk]);
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      acc = __builtin_fmaf(__uint_as_float(ov[w] << 16), __uint_as_float(dv[w] << 16), acc);
-      acc = __builtin_fmaf(__uint_as_float(ov[w] & 0xffff0000u), __uint_as_float(dv[w] & 0xffff0000u), acc);
+      acc = __builtin_fmaf(__uint_as_float(a[w] << 16), __uint_as_float(b[w] << 16), acc);
+      acc = __builtin_fmaf(__uint_as_float(a[w] & 0xffff0000u), __uint_as_float(b[w] & 0xffff0000u), acc);
     }
   }
-  const int ir = udiv(i, p.div_dil), r = i - ir * p.mask.dil;
-  const int64_t o2 = ((int64_t)bh * p.residues + r) * p.SR + ir;
-  const int64_t plane = (int64_t)p.B * p.H * p.residues * p.SR;
-  p.stats[o2] = p.lse[b * p.lse_sb + h * p.lse_sh + t * p.lse_ss] * kLog2e;
-  // delta times the head's score scale c1: ds = p (dp c1 - delta c1) is then one fma and a multiply
-  p.stats[plane + o2] = acc * (p.scale * (p.head_scale ? p.head_scale[h] : 1.0f));
+  return acc;
 }
+
 
 // ---- dQ ------------------------------------------------------------------------
 template <int D, int NORM, bool ALIBI, bool SOFTCAP>
@@ -303,11 +285,14 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
       df[kk] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(ds + 16 * kk));
     }
   }
-  float lse2 = 0.f, delta = 0.f;
+  // softmax row statistics: the lane's half row of O, loaded beside Q and dO;
+  // the row's lse and the arithmetic follow the DMA prologue
+  bf16x8_t of[DK];
+  float lse2 = 0.f, ndelta = 0.f;
   if constexpr (NORM == NORM_SOFTMAX) {
-    const int64_t o2 = ((int64_t)(b * p.H + h) * p.residues + r) * p.SR + (ok ? i : 0);  // b: the sequence
-    lse2 = p.stats[o2];
-    delta = p.stats[(int64_t)p.B * p.H * p.residues * p.SR + o2];
+    const uint16_t* os = p.o + b * p.o_sb + h * p.o_sh + (t0 + (int64_t)(ok ? i : 0) * dil) * p.o_ss + 8 * lh;
+#pragma unroll
+    for (int kk = 0; kk < DK; ++kk) of[kk] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(os + 16 * kk));
   }
 
   // key tiles of the workgroup's rows; per-wavefront classification bounds
@@ -344,7 +329,19 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   // also drains the K/V tiles in flight (the compiler does not count the DMA)
 #pragma unroll
   for (int kk = 0; kk < DK; ++kk) asm volatile("" : "+v"(qf[kk]), "+v"(df[kk]));
-  asm volatile("" : "+v"(lse2), "+v"(delta));
+  if constexpr (NORM == NORM_SOFTMAX) {
+    // lse log2 e, and -delta (the dP accumulators' seed) from do . o: this
+    // lane's half row, then its partner's (lane ^ 32); stored for dK/dV
+    lse2 = p.lse[b * p.lse_sb + h * p.lse_sh + (t0 + (int64_t)(ok ? i : 0) * dil) * p.lse_ss] * kLog2e;
+    const float part = half_row_dot<DK>(df, of);
+    ndelta = -(part + __shfl_xor(part, 32));
+    if (ok && lh == 0) {
+      const int64_t o2 = ((int64_t)(b * p.H + h) * p.residues + r) * p.SR + i;  // b: the sequence
+      p.stats[o2] = lse2;
+      p.stats[(int64_t)p.B * p.H * p.residues * p.SR + o2] = ndelta;
+    }
+    asm volatile("" : "+v"(lse2), "+v"(ndelta));
+  }
 
   typedef short i16x8_t __attribute__((ext_vector_type(8)));
   for (int it = 0; it < ntiles; ++it) {
@@ -363,7 +360,10 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
     for (int kb = 0; kb < KB; ++kb) {
       f32x16_t sacc, pacc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.f;
+      for (int e = 0; e < 16; ++e) {
+        sacc[e] = 0.f;
+        pacc[e] = NORM == NORM_SOFTMAX ? ndelta : 0.f;
+      }
       if constexpr (kSeed) {  // register e: key jt0 + 32 kb + 4 lh + rc(e), query i
         const float b0 = sg.bq * (float)(jt0 + 32 * kb + 4 * lh - i);
 #pragma unroll
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float pv;
-        sg(sacc[e], pacc[e], (float)(jbase + 8 * (e >> 2) + (e & 3) - i), lse2, delta, pv, ds[e]);
+        sg(sacc[e], pacc[e], (float)(jbase + 8 * (e >> 2) + (e & 3) - i), lse2, pv, ds[e]);
       }
       if (cls == TILE_PARTIAL) zero_hidden(ds, hidden_bits(g, i, jbase));
 #pragma unroll
@@ -404,8 +404,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   }
 
   if (ok) {
-    // sigmoid / ReLU ds was accumulated without the head's scale (softmax's includes it)
-    const float c1 = NORM == NORM_SOFTMAX ? 1.0f : sg.c1;
+    // ds was accumulated without the head's scale
+    const float c1 = sg.c1;
     uint16_t* dst = dqh + (int64_t)i * dqrs + 4 * lh;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -420,11 +420,14 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
 }
 
 // ---- dK, dV ----------------------------------------------------------------------
-template <int D, int NORM, bool ALIBI, bool SOFTCAP>
+// HEAD_C1: the query heads of a K/V group differ in score scale (GQA with
+// per-head scales), so c1 multiplies each score; otherwise it multiplies dK
+// once at the store.
+template <int D, int NORM, bool ALIBI, bool SOFTCAP, bool HEAD_C1>
 __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(const BwdParams p) {
   constexpr int NW = 4, BM = 64, QB = BM / 32, DK = D / 16, DB = D / 32;
   constexpr int RP = 2 * D, T_BYTES = BM * RP;
-  // stage: Q tile, dO tile, then (softmax) the 64 rows' lse log2 e and delta
+  // stage: Q tile, dO tile, then (softmax) the 64 rows' lse log2 e and -delta
   constexpr bool kStats = NORM == NORM_SOFTMAX;
   constexpr int STAGE_BYTES = 2 * T_BYTES + (kStats ? 512 : 0);
   constexpr int NS = 3;
@@ -475,6 +478,9 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     head_c[kMaxGroup + t] = (ALIBI && p.alibi_slopes) ? p.alibi_slopes[hq] * (float)p.mask.dil : 0.0f;
   }
   __syncthreads();
+  // ds leaves the score step without c1: applied to dK at the store when the
+  // group shares one scale, else per score
+  const float c1u = HEAD_C1 ? 1.0f : head_c[0];
 
   // this wavefront's 32 keys: K and V as MFMA B operands (lane = key)
   const int key0 = blk * 128 + 32 * wave;
@@ -546,7 +552,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     dma_rows<D, NW>(dc.dob, dors, i0, g.S, st + T_BYTES, wave, lane);
     if constexpr (kStats) {
       // wavefront w moves 32 floats: lse log2 e rows [32 w, +32) (w < 2), or
-      // delta rows [32 (w - 2), +32); the stats rows are padded to 64
+      // -delta rows [32 (w - 2), +32); the stats rows are padded to 64
       const float* src = dc.sb + (wave >= 2 ? plane : 0) + i0 + 32 * (wave & 1);
       if (lane < 32) dma4s(src, (uint32_t)(4 * lane), lds_addr(st + 2 * T_BYTES + 128 * wave));
     }
@@ -576,13 +582,27 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     constexpr bool kSeed = ALIBI && !SOFTCAP;  // as in the dQ kernel
     ScoreGrad<NORM, ALIBI && !kSeed, SOFTCAP> sg = score_consts<NORM, ALIBI && !kSeed, SOFTCAP>(p);
     sg.set_head(head_c[hq - hkv * p.G], head_c[kMaxGroup + hq - hkv * p.G]);
-    const float* st_stats = (const float*)(St + 2 * T_BYTES);  // [64] lse log2 e, then [64] delta
+    const float* st_stats = (const float*)(St + 2 * T_BYTES);  // [64] lse log2 e, then [64] -delta
 
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
+      // rows of register e: ibase + 8 (e >> 2) + (e & 3); softmax: their lse
+      // log2 e, and -delta as the dP accumulator's seed
+      const int ibase = i0 + 32 * qb + 4 * lh;
+      f32x4_t l4[4], d4[4];
+      if constexpr (kStats) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          l4[gq] = *(const f32x4_t*)(st_stats + 32 * qb + 4 * lh + 8 * gq);
+          d4[gq] = *(const f32x4_t*)(st_stats + 64 + 32 * qb + 4 * lh + 8 * gq);
+        }
+      }
       f32x16_t sacc, pacc;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[e] = pacc[e] = 0.f;
+      for (int e = 0; e < 16; ++e) {
+        sacc[e] = 0.f;
+        pacc[e] = kStats ? d4[e >> 2][e & 3] : 0.f;
+      }
       if constexpr (kSeed) {  // register e: query i0 + 32 qb + 4 lh + rc(e), key j
         const float b0 = sg.bq * (float)(j - (i0 + 32 * qb + 4 * lh));
 #pragma unroll
@@ -595,24 +615,16 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, kf[kk], sacc, 0, 0, 0);
         pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ad, vf[kk], pacc, 0, 0, 0);
       }
-      // rows of register e: ibase + 8 (e >> 2) + (e & 3)
-      const int ibase = i0 + 32 * qb + 4 * lh;
-      f32x4_t l4[4], d4[4];
-      if constexpr (kStats) {
-#pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          l4[gq] = *(const f32x4_t*)(st_stats + 32 * qb + 4 * lh + 8 * gq);
-          d4[gq] = *(const f32x4_t*)(st_stats + 64 + 32 * qb + 4 * lh + 8 * gq);
-        }
-      }
       float pv[16], dsv[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int rc = 8 * (e >> 2) + (e & 3);
-        const float ls = NORM == NORM_SOFTMAX ? l4[e >> 2][e & 3] : 0.f;
-        const float dl = NORM == NORM_SOFTMAX ? d4[e >> 2][e & 3] : 0.f;
-        sg(sacc[e], pacc[e], (float)(j - (ibase + rc)), ls, dl, pv[e], dsv[e]);
-        if constexpr (NORM != NORM_SOFTMAX) dsv[e] *= sg.c1;  // the group's heads may differ in scale
+        const float ls = kStats ? l4[e >> 2][e & 3] : 0.f;
+        sg(sacc[e], pacc[e], (float)(j - (ibase + rc)), ls, pv[e], dsv[e]);
+      }
+      if constexpr (HEAD_C1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) dsv[e] *= sg.c1;
       }
       if (cls == TILE_PARTIAL) {
         // bit k: row ibase + k does not see key j
@@ -658,8 +670,8 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2_t wk, wv;
-        wk[0] = pack_bf16x2(dk[db][4 * gq + 0], dk[db][4 * gq + 1]);
-        wk[1] = pack_bf16x2(dk[db][4 * gq + 2], dk[db][4 * gq + 3]);
+        wk[0] = pack_bf16x2(dk[db][4 * gq + 0] * c1u, dk[db][4 * gq + 1] * c1u);
+        wk[1] = pack_bf16x2(dk[db][4 * gq + 2] * c1u, dk[db][4 * gq + 3] * c1u);
         wv[0] = pack_bf16x2(dv[db][4 * gq + 0], dv[db][4 * gq + 1]);
         wv[1] = pack_bf16x2(dv[db][4 * gq + 2], dv[db][4 * gq + 3]);
         *(u32x2_t*)(kdst + 32 * db + 8 * gq) = wk;
