@@ -190,8 +190,10 @@ int chia_attn_bwd(const chia_attn_bwd_args* args, void* stream);
  * `stream` current.  Every call on one GPU shares that GPU's array: calls that
  * overlap in time on one GPU (other streams, other host threads) race and must
  * be serialised by the caller.  Nothing in the array needs clearing between
- * calls (each call writes every statistic it reads).  Results are those of
- * chia_attn_bwd bit for bit (the same kernels). */
+ * calls: each call writes the statistics of every row it has before any
+ * kernel reads them, and the padding rows of a last partial tile, which are
+ * read, never reach a result.  Results are those of chia_attn_bwd bit for bit
+ * (the same kernels). */
 #define CHIA_ATTN_NOALLOC_SCRATCH_BYTES (8 << 20)
 int chia_attn_bwd_noalloc(const chia_attn_bwd_args* args, void* stream);
 

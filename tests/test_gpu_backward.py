@@ -86,6 +86,13 @@ EDGE = [
     ("gqa_causal_g2", 1, 4, 2, 640, 64, dict(causal=True)),
     ("mqa_window_g4", 2, 4, 1, 300, 64, dict(causal=True, window=70)),
     ("gqa_sigmoid_g2_d128", 1, 4, 2, 256, 128, dict(norm="sigmoid", causal=False, bias=-2.0)),
+    # per-head scales that differ inside a K/V group: dK takes c1 per score
+    ("gqa_headscale_g2", 1, 4, 2, 640, 64, dict(causal=True, head_scale=[0.5, 2.0, 1.0, 0.25])),
+    ("gqa_headscale_sigmoid_d128", 1, 4, 2, 256, 128, dict(norm="sigmoid", causal=False, bias=-2.0,
+                                                             head_scale=[1.0, 0.5, 2.0, 2.0])),
+    ("mqa_headscale_relu_alibi", 1, 4, 1, 300, 64, dict(norm="relu", causal=True, post_scale=0.05,
+                                                        head_scale=[1.0, 0.5, 0.25, 2.0],
+                                                        alibi_slopes=[0.1, 0.05, 0.02, 0.01])),
 ]
 
 
