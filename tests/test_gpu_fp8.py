@@ -2,10 +2,13 @@
 
 Reference: attention of the dequantised e4m3 (or e5m2) inputs
 (oracle/fp8.py::fp8_ref, fp32).  Gate (per (b, h) slice, relative to s = max(1, max |ref|)): the
-kernel's error may exceed twice the error of the FP8 rounding model
-(oracle/fp8.py::fp8_emulated: the weights rounded to e4m3 after scaling by
-2^8) by at most the bf16 gate -- max 2e-2 s, mean 2e-3 s.  FP8 is the gate
-"widened accordingly": the widening is measured, not chosen."""
+kernel's error against it may be at most twice the max error and 1.25 times the mean error of the
+FP8 rounding model (oracle/fp8.py::fp8_emulated: the weights rounded to e4m3 after scaling by 2^8),
+plus a fifth of the bf16 gate (max 4e-3 s, mean 4e-4 s).  The kernel rounds the softmax weights
+against its running row maximum and the model against the exact one, so the two errors differ
+slightly: over every case below the kernel stays within 1.87x the model's max error and 1.07x its
+mean error.  (The gate used to allow twice the model's errors plus the whole bf16 gate, 2e-2 s and
+2e-3 s, which a kernel with no FP8 rounding fault at all could have spent.)"""
 import pytest
 import torch
 
@@ -42,9 +45,9 @@ def _check(name, qkv, kw):
             s = max(1.0, r.abs().max().item())
             e_k = (got[b, h] - r).abs()
             e_m = (emu[b, h] - r).abs()
-            assert e_k.max().item() <= 2 * e_m.max().item() + 2e-2 * s, (name, b, h, e_k.max().item(), e_m.max().item())
-            assert e_k.mean().item() <= 2 * e_m.mean().item() + 2e-3 * s, (name, b, h, e_k.mean().item(),
-                                                                           e_m.mean().item())
+            assert e_k.max().item() <= 2 * e_m.max().item() + 4e-3 * s, (name, b, h, e_k.max().item(), e_m.max().item())
+            assert e_k.mean().item() <= 1.25 * e_m.mean().item() + 4e-4 * s, (name, b, h, e_k.mean().item(),
+                                                                              e_m.mean().item())
     return o
 
 

@@ -164,14 +164,15 @@ def test_random_fp8_case(seed):
     assert o.shape == (B, H, S, D) and bool(torch.isfinite(got).all())
     ref = fp8_ref(q8, k8, v8, qd, kd, vd, **kw)
     emu = fp8_emulated(q8, k8, v8, qd, kd, vd, **kw)
-    # the FP8 suite's gate (tests/test_gpu_fp8.py): twice the rounding model's error plus the bf16 gate
+    # the FP8 suite's gate (tests/test_gpu_fp8.py): twice the rounding model's max error and 1.25
+    # times its mean error, plus a fifth of the bf16 gate
     for b in range(B):
         for h in range(H):
             r = ref[b, h]
             sc = max(1.0, r.abs().max().item())
             e_k, e_m = (got[b, h] - r).abs(), (emu[b, h] - r).abs()
-            assert e_k.max().item() <= 2 * e_m.max().item() + 2e-2 * sc, (seed, b, h, e_k.max().item())
-            assert e_k.mean().item() <= 2 * e_m.mean().item() + 2e-3 * sc, (seed, b, h, e_k.mean().item())
+            assert e_k.max().item() <= 2 * e_m.max().item() + 4e-3 * sc, (seed, b, h, e_k.max().item())
+            assert e_k.mean().item() <= 1.25 * e_m.mean().item() + 4e-4 * sc, (seed, b, h, e_k.mean().item())
 
 
 # 600005 (ReLU with softcap): a score at u = 6.5e-7 lost its derivative where
