@@ -51,13 +51,22 @@ def median_us(fn: Callable[[], object], rounds: int = 3, **kw) -> float:
 
 
 class CacheFlusher:
-    """Writes a buffer larger than the 256 MB Infinity Cache to evict q/k/v/o."""
+    """Evicts q/k/v/o by reading a buffer larger than the 256 MB Infinity Cache.
+
+    Reading leaves the caches holding clean lines.  Writing the buffer instead
+    leaves up to a cache's worth of dirty lines, whose write-back then runs
+    inside the next measured kernel and competes with its reads: at B4 H16
+    S4096 D64 that added 10-26 us to the banded kernels' cold times (local
+    45.0 against 55.6 us, block-diagonal 39.0 against 56.5 us).  Reading a 1 GB
+    buffer, or two 512 MB buffers in turn, gives the same times as this one.
+    """
 
     def __init__(self, nbytes: int = 512 << 20, device: str = "cuda"):
-        self.buf = torch.empty(nbytes // 4, dtype=torch.float32, device=device)
+        self.buf = torch.ones(nbytes // 4, dtype=torch.float32, device=device)
+        self.acc = torch.zeros(1, dtype=torch.float32, device=device)
 
     def __call__(self) -> None:
-        self.buf.fill_(1.0)
+        torch.sum(self.buf, dim=(0,), out=self.acc[0])
 
 
 def cold_us(fn: Callable[[], object], reps: int = 20, flusher: CacheFlusher = None) -> float:
