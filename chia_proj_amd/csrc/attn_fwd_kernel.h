@@ -265,6 +265,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   // adding the bias afterwards.  Softmax then runs the plain exponent.
   constexpr bool kBiasInit = ALIBI && !SOFTCAP;
   constexpr bool kScaledSoftmax = kPlainSoftmax || (kBiasInit && NORM == NORM_SOFTMAX);  // exponent fma(s, kq, -m)
+  constexpr bool kBiasFold = kBiasInit && NORM == NORM_SOFTMAX;  // the block bias in the exponent (below)
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
   // Softcapped softmax keeps r = 1 / (1 + 2^(2 s log2e / cap)) per score; the
   // capped score in log2 units is t = sc_a r + sc_b (sc_a < 0), folded into
@@ -368,6 +369,14 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
   }
   const float post = kRawRelu ? p.post_scale * c1 : p.post_scale;
   const float bq = kBiasInit ? sl / c1 : 0.f;  // ALiBi bias per key step, in units of q . k
+  // ALiBi softmax: S starts from bq rc(e), the bias of register e's key
+  // offset rc(e) inside a 32-key block (the same registers for every block),
+  // and the rest, bq (j0 - i) for the block's first key j0 and the lane's row
+  // i, joins the exponent as one constant per block.  (ALiBi sigmoid / ReLU
+  // seed S with the whole bias: their kernels have no registers to spare.)
+  f32x16_t bias_rc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) bias_rc[e] = kBiasFold ? bq * (float)(8 * (e >> 2) + (e & 3)) : 0.f;
   // Plain sigmoid: Q is pre-scaled by kq (one bf16 rounding per element, at
   // load), so a score is already the exponent, and the bias enters as the
   // factor 2^k0: p = 1 / (1 + 2^k0 2^s).  The host routes a bias whose 2^k0
@@ -592,13 +601,19 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
     // key block kb (0 .. NKB-1) of the step: its stage and first row there
     auto kb_base = [&](int kb) { return (kb < KB ? St : St2) + 32 * (kb % KB) * RP; };
     f32x16_t sacc[NSTR];
+    float bias0[NSTR];  // ALiBi softmax: bq (j0 - i) of the stream's block (scores are sacc + bias0)
 #pragma unroll
     for (int st = 0; st < NSTR; ++st) {
-      if constexpr (kBiasInit) {
+      if constexpr (kBiasFold) {
+        bias0[st] = bq * (float)(jt0 + 32 * kb_of(st) + 4 * lh - (row0[qb_of(st)] + lq));
+        sacc[st] = bias_rc;
+      } else if constexpr (kBiasInit) {
+        bias0[st] = 0.f;
         const float b0 = bq * (float)(jt0 + 32 * kb_of(st) + 4 * lh - (row0[qb_of(st)] + lq));
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[st][e] = __builtin_fmaf(bq, (float)(8 * (e >> 2) + (e & 3)), b0);
       } else {
+        bias0[st] = 0.f;
 #pragma unroll
         for (int e = 0; e < 16; ++e) sacc[st][e] = 0.f;
       }
@@ -690,13 +705,14 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
         for (int st = 0; st < NSTR; ++st) {
           const int qb = qb_of(st);
           const float m_use = (m_run[qb] == -INFINITY) ? 0.f : m_run[qb];
+          const float moff = kBiasFold ? __builtin_fmaf(bias0[st], kq, -m_use) : -m_use;
           float ls = lt[qb];
 #pragma unroll
           for (int w = 0; w < 8; ++w) {
             float p0, p1;
             if constexpr (kScaledSoftmax) {
-              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, -m_use));
-              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, -m_use));
+              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], kq, moff));
+              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], kq, moff));
             } else if constexpr (kCapR) {
               p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w], sc_a, sc_b - m_use));
               p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[st][2 * w + 1], sc_a, sc_b - m_use));
@@ -739,6 +755,7 @@ __global__ __launch_bounds__(NW * 64, Occupancy<D>::value) void attn_fwd_kernel(
           } else {
 #pragma unroll
             for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sacc[st][e]);
+            if constexpr (kBiasFold) mx += bias0[st];
           }
           mq[qb_of(st)] = fmaxf(mq[qb_of(st)], mx);
         }

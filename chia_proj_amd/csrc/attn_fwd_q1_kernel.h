@@ -74,6 +74,8 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
   constexpr bool kPlainSoftmax = (NORM == NORM_SOFTMAX) && !ALIBI && !SOFTCAP;
   constexpr bool kBiasInit = ALIBI && !SOFTCAP;
   constexpr bool kScaledSoftmax = kPlainSoftmax || (kBiasInit && NORM == NORM_SOFTMAX);
+  // the step's bias in the exponent (below): ALiBi softmax at head dim 128
+  constexpr bool kBiasFold = kBiasInit && NORM == NORM_SOFTMAX && D == 128;
   constexpr bool kRawRelu = (NORM == NORM_RELU) && !ALIBI && !SOFTCAP;
   constexpr bool kCapR = SOFTCAP && NORM == NORM_SOFTMAX;
   constexpr bool kSigFold = NORM == NORM_SIGMOID && !ALIBI && !SOFTCAP;
@@ -162,6 +164,14 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
   }
   const float post = kRawRelu ? p.post_scale * c1 : p.post_scale;
   const float bq = kBiasInit ? sl / c1 : 0.f;
+  // ALiBi softmax at head dim 128: S starts from bq rc(e), the bias of
+  // register e's key offset inside a 32-key step (the same registers for
+  // every step); the rest, bq (j0 - i), joins the exponent once per step.
+  // (Elsewhere S starts from the whole bias: at head dim 64 the four
+  // wavefronts per SIMD leave no registers to spare.)
+  f32x16_t bias_rc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) bias_rc[e] = kBiasFold ? bq * (float)(8 * (e >> 2) + (e & 3)) : 0.f;
   const float sig_c =
       kSigFold ? __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(__builtin_amdgcn_exp2f(k0)))) : 0.f;
 
@@ -332,7 +342,11 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
         if (cls == TILE_EMPTY) continue;
         const char* Kb = St + 32 * kb * RP;
         f32x16_t s;
-        if constexpr (kBiasInit) {
+        float bias0 = 0.f;  // ALiBi softmax: bq (j0 - i) of this step (scores are s + bias0)
+        if constexpr (kBiasFold) {
+          bias0 = bq * (float)(jb + 4 * lh - i);
+          s = bias_rc;
+        } else if constexpr (kBiasInit) {
           const float b0 = bq * (float)(jb + 4 * lh - i);
 #pragma unroll
           for (int e = 0; e < 16; ++e) s[e] = __builtin_fmaf(bq, (float)(8 * (e >> 2) + (e & 3)), b0);
@@ -403,6 +417,7 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
           } else {
 #pragma unroll
             for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
+            if constexpr (kBiasFold) mx += bias0;
           }
           mx = xhalf_max(mx);
           if constexpr (kScaledSoftmax) mx = mx * kq;
@@ -417,13 +432,14 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
             m_run = m_new;
           }
           const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+          const float moff = kBiasFold ? __builtin_fmaf(bias0, kq, -m_use) : -m_use;
           float ls = l_run;
 #pragma unroll
           for (int w = 0; w < 8; ++w) {
             float p0, p1;
             if constexpr (kScaledSoftmax) {
-              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], kq, -m_use));
-              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], kq, -m_use));
+              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], kq, moff));
+              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], kq, moff));
             } else if constexpr (kCapR) {
               p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], sc_a, sc_b - m_use));
               p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], sc_a, sc_b - m_use));
