@@ -32,10 +32,10 @@
 //     DMA runs across the boundary between the two blocks of a pair;
 //   * a tile is computed as two 32-key steps: S^T = K Q^T (D / 16 MFMAs),
 //     score modifier, mask on partial steps, normaliser with its own row-max
-//     update, then O^T += V^T P^T (D / 16 MFMAs), with the matrix-core layouts
-//     of the paired core (lane = query column; V^T read with
-//     ds_read_b64_tr_b16); a 32-key step that no row of the wavefront sees is
-//     skipped.
+//     update (lazy at head_dim 64), then O^T += V^T P^T (D / 16 MFMAs), with
+//     the matrix-core layouts of the paired core (lane = query column; V^T
+//     read with ds_read_b64_tr_b16); a 32-key step that no row of the
+//     wavefront sees is skipped.
 #pragma once
 #include "attn_fwd_kernel.h"
 
@@ -409,49 +409,74 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
         // normaliser -> p, packed to bf16 pairs
         uint32_t pk[8];
         if constexpr (NORM == NORM_SOFTMAX) {
-          float mx = s[0];
-          if constexpr (kCapR) {
+          // head_dim 64: the lazy row max of the paired core.  The step's
+          // weights are first taken against the running max m; only when a
+          // row has no max yet, or some lane's partial row sum over the step
+          // exceeds kLazyBound (a weight may exceed it), is the step's max
+          // taken, m raised when it exceeds m by more than kRescaleLog2, and
+          // the weights recomputed.  So p <= kLazyBound.  At head_dim 128
+          // (two wavefronts per SIMD) the per-step max measured faster.
+          constexpr bool kLazy = D == 64;
+          // weights of the step against m_use into pk; lt = start + their
+          // lane's row sum
+          auto exps = [&](float m_use, float start, float& lt) __attribute__((always_inline)) {
+            const float moff = kBiasFold ? __builtin_fmaf(bias0, kq, -m_use) : -m_use;
+            float ls = start;
 #pragma unroll
-            for (int e = 1; e < 16; ++e) mx = fminf(mx, s[e]);
-            mx = __builtin_fmaf(mx, sc_a, sc_b);
-          } else {
-#pragma unroll
-            for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
-            if constexpr (kBiasFold) mx += bias0;
-          }
-          mx = xhalf_max(mx);
-          if constexpr (kScaledSoftmax) mx = mx * kq;
-          const float m_new = (mx > m_run + kRescaleLog2) ? mx : m_run;
-          if (__any(m_new != m_run)) {
-            const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-              for (int e = 0; e < 16; ++e) oacc[db][e] *= alpha;
-            m_run = m_new;
-          }
-          const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-          const float moff = kBiasFold ? __builtin_fmaf(bias0, kq, -m_use) : -m_use;
-          float ls = l_run;
-#pragma unroll
-          for (int w = 0; w < 8; ++w) {
-            float p0, p1;
-            if constexpr (kScaledSoftmax) {
-              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], kq, moff));
-              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], kq, moff));
-            } else if constexpr (kCapR) {
-              p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], sc_a, sc_b - m_use));
-              p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], sc_a, sc_b - m_use));
-            } else {
-              p0 = __builtin_amdgcn_exp2f(s[2 * w] - m_use);
-              p1 = __builtin_amdgcn_exp2f(s[2 * w + 1] - m_use);
+            for (int w = 0; w < 8; ++w) {
+              float p0, p1;
+              if constexpr (kScaledSoftmax) {
+                p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], kq, moff));
+                p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], kq, moff));
+              } else if constexpr (kCapR) {
+                p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w], sc_a, sc_b - m_use));
+                p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[2 * w + 1], sc_a, sc_b - m_use));
+              } else {
+                p0 = __builtin_amdgcn_exp2f(s[2 * w] - m_use);
+                p1 = __builtin_amdgcn_exp2f(s[2 * w + 1] - m_use);
+              }
+              const bf16x2_t pb = pack2(p0, p1);
+              ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);
+              pk[w] = __builtin_bit_cast(uint32_t, pb);
             }
-            const bf16x2_t pb = pack2(p0, p1);
-            ls = __builtin_amdgcn_fdot2_f32_bf16(pb, kOnes2, ls, false);
-            pk[w] = __builtin_bit_cast(uint32_t, pb);
+            lt = ls;
+          };
+          float lt = 0.f;
+          bool exact = true;
+          if constexpr (kLazy) {
+            exact = __any(m_run == -INFINITY);
+            if (!exact) {
+              exps(m_run, 0.f, lt);
+              exact = __any(!(lt <= kLazyBound));
+            }
           }
-          l_run = ls;
+          if (exact) {
+            float mx = s[0];
+            if constexpr (kCapR) {
+#pragma unroll
+              for (int e = 1; e < 16; ++e) mx = fminf(mx, s[e]);
+              mx = __builtin_fmaf(mx, sc_a, sc_b);
+            } else {
+#pragma unroll
+              for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s[e]);
+              if constexpr (kBiasFold) mx += bias0;
+            }
+            mx = xhalf_max(mx);
+            if constexpr (kScaledSoftmax) mx = mx * kq;
+            const float m_new = (mx > m_run + kRescaleLog2) ? mx : m_run;
+            if (__any(m_new != m_run)) {
+              const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+              l_run *= alpha;
+#pragma unroll
+              for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) oacc[db][e] *= alpha;
+              m_run = m_new;
+            }
+            const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+            exps(m_use, kLazy ? 0.f : l_run, lt);
+          }
+          l_run = kLazy ? l_run + lt : lt;
         } else {
 #pragma unroll
           for (int w = 0; w < 8; ++w) {

@@ -157,6 +157,8 @@ RISING = [
     ("headscale", dict(causal=True, head_scale="per-head")),
     ("window256", dict(causal=True, window=256)),
     ("block256", dict(causal=False, block=256)),
+    ("window200_softcap30", dict(causal=True, window=200, softcap=30.0)),
+    ("local100_dil2", dict(causal=False, window=100, dilation=2)),
 ]
 
 
@@ -178,8 +180,8 @@ def test_alibi_softmax_tile_order(name, kw, sign, shape, D):
     """ALiBi softmax walks the key tiles from the last to the first (both cores; the paired
     core also takes the row max only on demand).  Steep slopes (up to 2 per key) with the
     standard sign put a row's max on its first tile; the negated slopes put it on the last one,
-    so the exact fallback (paired core) or the rescale (one-block core) runs on almost every
-    tile.  Prefix tiles come after the band tiles in that order.  At head dim 64 the smaller
+    so the exact fallback (paired core, one-block core at head dim 64) or the rescale (one-block
+    core at head dim 128) runs on almost every tile.  Prefix tiles come after the band tiles in that order.  At head dim 64 the smaller
     shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones (PAIR,
     WIDE and WIDE2 steps), and the window / block masks the one-block core; head dim 128 runs
     the one-block core."""
@@ -206,8 +208,9 @@ def test_softmax_rising_scores(name, kw, shape, D):
     plus noise, so a row's max climbs ~23 log2-units per 64-key tile at either head dim.  The
     paired core first computes a tile's softmax weights against the running reference max and,
     when a partial row sum over the tile exceeds 2^16, recomputes them against the new max; these
-    inputs take that path on almost every tile.  The one-block core takes the exact row max of
-    every 32-key step, so here they drive its per-step rescale of O and l.  At head dim 64 the
+    inputs take that path on almost every tile.  The one-block core does the same per 32-key step
+    at head dim 64; at head dim 128 it takes the exact row max of every step, so here they drive
+    its per-step rescale of O and l.  At head dim 64 the
     smaller shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones
     (PAIR, WIDE and WIDE2 steps), and the window / block masks run the one-block core; at head
     dim 128 every case runs the one-block core."""
