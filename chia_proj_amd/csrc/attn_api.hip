@@ -140,7 +140,8 @@ Geometry paired_geometry(const MaskSpec& m, int64_t batch, int64_t heads) {
 }
 
 // The forward's core and geometry.  Head dim 64: the paired core, or for a
-// window or block mask the one-block core at four wavefronts per SIMD (north
+// window or block mask, causal rows with a prefix, and causal softmax on the
+// grids named below, the one-block core at four wavefronts per SIMD (north
 // star: local 53.2 -> 42.6 us, sliding window 53.1 -> 42.9, block-diagonal
 // 39.0 -> 30.5, dilated 61.6 -> 57.5; cold-cache 12-20 % less).  Head dim
 // 128: the one-block core (two wavefronts per SIMD), except for sigmoid and
@@ -162,18 +163,39 @@ Geometry forward_geometry(const chia_attn_args* a, const MaskSpec& m, const Scor
   // balance.  At head dim 64 such rows run the one-block core, one block per
   // workgroup, the blocks with the most keys launched first (prefix-LM 1024,
   // B4 H16 D64: 173.3 -> 164.0 us at S4096, 62.6 -> 56.9 us at S2048; the same
-  // order on the paired core, 166.0 / 62.3 us).  Plain causal rows keep the
-  // zigzag pairs: the one-block core launched longest-first measured within
-  // 3 % of them (temperature 156.8 -> 159.3 us, softcap 217.5 -> 211.9 us).
+  // order on the paired core, 166.0 / 62.3 us).
   const bool prefix_causal = geo.zigzag && m.prefix > 0;
-  if (a->head_dim == 64 && !banded && !prefix_causal) return geo;
+  // Plain causal softmax at head dim 64 runs the one-block core too, blocks
+  // longest-first, on the grids where it measured faster than the zigzag pairs
+  // (temperature + ALiBi + softcap, us, one process):
+  //   * pairs on 2-wavefront workgroups (too few rows for two 4-wavefront ones
+  //     per CU) and at least two one-block workgroups per CU: B4 H16 S1024
+  //     97.6 -> 79.6, B2 H16 S2048 164.2 -> 136.0, B1 H16 S4096 302.5 -> 252.8;
+  //     with fewer, slower (B1 H8 S2048, 128 workgroups: 122.7 -> 131.8);
+  //   * at least 64 (batch, head, residue) slices of at most 4096 rows:
+  //     B4 H16 S2048 169.8 -> 166.7, B4 H16 S4096 534.0 -> 517.5, B8 H32 S1024
+  //     195.5 -> 172.1; with 32 slices slower (B2 H16 S4096 294.5 -> 312.9),
+  //     and at 8192 rows slower or even (B1 H16 524.1 -> 578.2, B4 H16
+  //     2023 -> 2032).
+  // Only where the longest-first order applies (it needs a multiple of 8
+  // slices and no packed sequences): in natural order the blocks' unequal work
+  // is not balanced.  Full rows keep the paired core (north star, temperature
+  // 281.3 -> 302.6 us).
+  bool causal_q1 = false;
+  if (a->head_dim == 64 && geo.zigzag && !prefix_causal && !banded && a->norm == CHIA_ATTN_NORM_SOFTMAX &&
+      s0 <= 4096 && !a->cu_seqlens) {
+    const int64_t slices = a->batch * a->heads * geo.residues;
+    const int64_t q1_wg = slices * ((s0 + 127) / 128);
+    causal_q1 = slices % 8 == 0 && (slices >= 64 || (geo.waves == 2 && q1_wg >= 2 * kCUs));
+  }
+  if (a->head_dim == 64 && !banded && !prefix_causal && !causal_q1) return geo;
   if (a->head_dim == 128 && a->norm != CHIA_ATTN_NORM_SOFTMAX && !geo.zigzag && !banded && s0 >= 2048 && !sp.alibi &&
       !sp.softcap && geo.waves == 4)
     return geo;
   geo.q1 = true;
   geo.waves = 4;
   geo.rows = 128;
-  if (a->head_dim == 64 && prefix_causal) {
+  if (a->head_dim == 64 && (prefix_causal || causal_q1)) {
     geo.zigzag = 0;
     geo.rank = true;
   }

@@ -159,16 +159,32 @@ def test_intervals_and_tile_classes_match_oracle(S, lib_built):
 
 
 def test_plan_geometry(lib_built):
-    # causal without a window pairs row blocks (i, n-1-i); every pair is one workgroup
-    p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, causal=True))
+    # causal sigmoid without a window pairs row blocks (i, n-1-i); every pair is one workgroup
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, norm="sigmoid", causal=True))
     assert p["waves"] == 4 and p["block_m"] == 256 and p["workgroups"] == 4 * 16 * 8
-    # a window or block mask, or causal rows with a prefix (whose block work
-    # zigzag pairs do not balance), runs the one-block core: 128-row blocks,
-    # one per workgroup, 32-key steps
+    # so does causal softmax on fewer than 64 (batch, head) slices of 4096 rows,
+    # on rows longer than 4096, and on a grid too small for two one-block
+    # workgroups per CU (the pairs then have 2 wavefronts)
+    p = _lib.plan(make_args(batch=2, heads=16, seqlen=4096, head_dim=64, causal=True))
+    assert (p["waves"], p["block_m"], p["workgroups"]) == (4, 256, 2 * 16 * 16)
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=8192, head_dim=64, causal=True))
+    assert (p["waves"], p["block_m"]) == (4, 256)
+    p = _lib.plan(make_args(batch=1, heads=8, seqlen=2048, head_dim=64, causal=True))
+    assert (p["waves"], p["block_m"], p["workgroups"]) == (2, 128, 8 * 16)
+    # a window or block mask, causal rows with a prefix (whose block work
+    # zigzag pairs do not balance), and causal softmax on 64 slices or on 2-wavefront
+    # pairs' grids with at least 512 blocks run the one-block core: 128-row
+    # blocks, one per workgroup, 32-key steps
     for kw in (dict(causal=True, window=256), dict(causal=False, block=256), dict(causal=True, window=129),
-               dict(causal=True, prefix=1024)):
+               dict(causal=True, prefix=1024), dict(causal=True), dict(causal=True, softcap=50.0, alibi=True)):
         p = _lib.plan(make_args(batch=4, heads=16, seqlen=2048, head_dim=64, **kw))
         assert (p["waves"], p["block_m"], p["block_n"], p["workgroups"]) == (4, 128, 32, 4 * 16 * 16)
+    for b, h, s in ((4, 16, 1024), (1, 16, 4096), (4, 16, 4096)):
+        p = _lib.plan(make_args(batch=b, heads=h, seqlen=s, head_dim=64, causal=True))
+        assert (p["waves"], p["block_m"], p["block_n"], p["workgroups"]) == (4, 128, 32, b * h * s // 128)
+    # full rows stay on the paired core
+    p = _lib.plan(make_args(batch=4, heads=16, seqlen=4096, head_dim=64, causal=False))
+    assert (p["waves"], p["block_m"], p["block_n"]) == (4, 256, 64)
     # every visible pair is inside a computed 32 x block_n step
     for kw in (dict(causal=True), dict(causal=True, window=256), dict(causal=False, block=256),
                dict(causal=True, dilation=2, window=1024), dict(causal=True, prefix=1024)):

@@ -173,18 +173,16 @@ ALIBI_ORDER = [
 ]
 
 
-@pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("shape", [(1, 2, 700), (4, 16, 2048)], ids=["B1H2S700", "B4H16S2048"])
-@pytest.mark.parametrize("name,kw,sign", ALIBI_ORDER, ids=[a[0] for a in ALIBI_ORDER])
-def test_alibi_softmax_tile_order(name, kw, sign, shape, D):
-    """ALiBi softmax walks the key tiles from the last to the first (both cores; the paired
-    core also takes the row max only on demand).  Steep slopes (up to 2 per key) with the
-    standard sign put a row's max on its first tile; the negated slopes put it on the last one,
-    so the exact fallback (paired core, one-block core at head dim 64) or the rescale (one-block
-    core at head dim 128) runs on almost every tile.  Prefix tiles come after the band tiles in that order.  At head dim 64 the smaller
-    shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones (PAIR,
-    WIDE and WIDE2 steps), and the window / block masks the one-block core; head dim 128 runs
-    the one-block core."""
+# Which core runs these shapes at head dim 64: B1 H2 (two slices) the paired core
+# on 2-wavefront workgroups; B4 H16 S2048 the paired core on 4-wavefront ones
+# (PAIR, WIDE and WIDE2 steps) for full rows, the one-block core for causal
+# softmax, prefixes, windows and blocks; B2 H16 S4096 (32 slices) the paired core
+# on 4-wavefront workgroups for causal rows too.  Head dim 128 runs the
+# one-block core throughout.
+PAIRED_CAUSAL = (2, 16, 4096)
+
+
+def _alibi_order_case(name, kw, sign, shape, D):
     B, H, S = shape
     _say(f"[parity] alibi tile order {name} {shape} D{D}")
     g = torch.Generator("cpu").manual_seed(S + 3 * len(name) + D)
@@ -200,20 +198,27 @@ def test_alibi_softmax_tile_order(name, kw, sign, shape, D):
         res = gate.north_star_gate(r[0, 0], oc[b, h])
         assert res.ok, f"{name} b={b} h={h}: {res.status} {res.stats}"
 
+
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("shape", [(1, 2, 512), (4, 16, 2048)], ids=["B1H2S512", "B4H16S2048"])
-@pytest.mark.parametrize("name,kw", RISING, ids=[r[0] for r in RISING])
-def test_softmax_rising_scores(name, kw, shape, D):
-    """Scores that rise along the keys: q ~ 4 sqrt(D/64) u, k_j ~ (j / 2) u (u a unit vector)
-    plus noise, so a row's max climbs ~23 log2-units per 64-key tile at either head dim.  The
-    paired core first computes a tile's softmax weights against the running reference max and,
-    when a partial row sum over the tile exceeds 2^16, recomputes them against the new max; these
-    inputs take that path on almost every tile.  The one-block core does the same per 32-key step
-    at head dim 64; at head dim 128 it takes the exact row max of every step, so here they drive
-    its per-step rescale of O and l.  At head dim 64 the
-    smaller shape runs 2-wavefront workgroups of the paired core, the larger 4-wavefront ones
-    (PAIR, WIDE and WIDE2 steps), and the window / block masks run the one-block core; at head
-    dim 128 every case runs the one-block core."""
+@pytest.mark.parametrize("shape", [(1, 2, 700), (4, 16, 2048)], ids=["B1H2S700", "B4H16S2048"])
+@pytest.mark.parametrize("name,kw,sign", ALIBI_ORDER, ids=[a[0] for a in ALIBI_ORDER])
+def test_alibi_softmax_tile_order(name, kw, sign, shape, D):
+    """ALiBi softmax walks the key tiles from the last to the first (both cores), with the row
+    max only on demand (paired core, one-block core at head dim 64).  Steep slopes (up to 2 per
+    key) with the standard sign put a row's max on its first tile; the negated slopes put it on
+    the last one, so the exact fallback (or, in the one-block core at head dim 128, the rescale)
+    runs on almost every tile.  Prefix tiles come after the band tiles in that order."""
+    _alibi_order_case(name, kw, sign, shape, D)
+
+
+@pytest.mark.parametrize("name,kw,sign", [a for a in ALIBI_ORDER if a[0].startswith("causal")],
+                         ids=[a[0] for a in ALIBI_ORDER if a[0].startswith("causal")])
+def test_alibi_softmax_tile_order_paired_causal(name, kw, sign):
+    """The same on causal rows of the paired core's 4-wavefront workgroups (B2 H16 S4096 D64)."""
+    _alibi_order_case(name, kw, sign, PAIRED_CAUSAL, 64)
+
+
+def _rising_case(name, kw, shape, D):
     B, H, S = shape
     _say(f"[parity] rising scores {name} {shape} D{D}")
     g = torch.Generator("cpu").manual_seed(S + len(name) + D)
@@ -238,6 +243,27 @@ def test_softmax_rising_scores(name, kw, shape, D):
         r = oracle.attention_ref(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], **kwh)
         res = gate.north_star_gate(r[0, 0], oc[b, h])
         assert res.ok, f"{name} b={b} h={h}: {res.status} {res.stats}"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("shape", [(1, 2, 512), (4, 16, 2048)], ids=["B1H2S512", "B4H16S2048"])
+@pytest.mark.parametrize("name,kw", RISING, ids=[r[0] for r in RISING])
+def test_softmax_rising_scores(name, kw, shape, D):
+    """Scores that rise along the keys: q ~ 4 sqrt(D/64) u, k_j ~ (j / 2) u (u a unit vector)
+    plus noise, so a row's max climbs ~23 log2-units per 64-key tile at either head dim.  The
+    paired core first computes a tile's softmax weights against the running reference max and,
+    when a partial row sum over the tile exceeds 2^16, recomputes them against the new max; these
+    inputs take that path on almost every tile.  The one-block core does the same per 32-key step
+    at head dim 64; at head dim 128 it takes the exact row max of every step, so here they drive
+    its per-step rescale of O and l."""
+    _rising_case(name, kw, shape, D)
+
+
+@pytest.mark.parametrize("name,kw", [r for r in RISING if r[0] in ("causal", "softcap50", "headscale")],
+                         ids=["causal", "softcap50", "headscale"])
+def test_softmax_rising_scores_paired_causal(name, kw):
+    """The same on causal rows of the paired core's 4-wavefront workgroups (B2 H16 S4096 D64)."""
+    _rising_case(name, kw, PAIRED_CAUSAL, 64)
 
 
 def test_strided_layout_and_out_param():
