@@ -1,6 +1,7 @@
 // attn_fwd_q1_kernel.h -- the one-block forward core: one 32-row query block
 // per wavefront.  It runs every head_dim 128 forward but long full rows of
-// sigmoid / ReLU, and the banded masks (window, block) at head_dim 64.
+// sigmoid / ReLU, and at head_dim 64 the banded masks (window, block), causal
+// rows with a prefix, and causal softmax on large grids.
 //
 // Reference semantics: the eager closures of extra_bench.py:32-62 and
 // sigmoid_fix.py:34-40, as for attn_fwd_kernel.h, whose helpers (DMA, LDS
@@ -18,7 +19,9 @@
 //     K/V reads.
 //   * head_dim 64, banded masks: a workgroup's key range is its rows plus the
 //     window, a few tiles; four wavefronts per SIMD (~110 VGPRs) hide the
-//     latency of those few tiles better than the paired core's two.
+//     latency of those few tiles better than the paired core's two.  Causal
+//     rows (a prefix, or softmax on large grids): one block per workgroup,
+//     launched longest-first, balances them where zigzag pairs measured slower.
 //
 // Work decomposition
 //   * a workgroup of 4 wavefronts owns row blocks of 128 rows of one (batch,
@@ -228,11 +231,14 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
     k_dma[n] = (uint32_t)(2 * ((int64_t)row * krs + 8 * k_slot<D>(row, slot)));
     v_dma[n] = (uint32_t)(2 * ((int64_t)row * vrs + 8 * v_slot<D>(row, slot)));
   }
-  auto issue_step = [&](int s) {
-    const int jt0 = step_key0(s);
-    char* kst = lds + (s % NS) * STAGE_BYTES;
-    const uint16_t* kt = kh + (int64_t)jt0 * krs;
-    const uint16_t* vt = vh + (int64_t)jt0 * vrs;
+  // The tile's row base in 32-bit unsigned arithmetic: keys and the K / V
+  // row strides (times the dilation) are non-negative and below 2^25.
+  static_assert((NS & (NS - 1)) == 0, "the stage index is a mask");
+  const uint32_t krs_u = (uint32_t)krs, vrs_u = (uint32_t)vrs;
+  auto issue_step = [&](int s, int jt0) {
+    char* kst = lds + ((uint32_t)s & (NS - 1)) * STAGE_BYTES;
+    const uint16_t* kt = kh + (uint64_t)(uint32_t)jt0 * krs_u;
+    const uint16_t* vt = vh + (uint64_t)(uint32_t)jt0 * vrs_u;
     if (jt0 + BN <= g.S) {
 #pragma unroll
       for (int n = 0; n < NDMA; ++n) {
@@ -252,9 +258,16 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
       }
     }
   };
-  // prologue: the first NS - 1 steps (each barrier issues one more)
+  // prologue: the first NS - 1 steps (each barrier issues one more).  With
+  // two stages one step is in flight: its first key, found for the DMA, is
+  // the compute's key one iteration later (jt_dma).
+  static_assert(NS == 2, "one step in flight");
   int dma_next = s_lo;
-  for (; dma_next < s_lo + NS - 1 && dma_next < s_hi; ++dma_next) issue_step(dma_next);
+  int jt_dma = 0;
+  for (; dma_next < s_lo + NS - 1 && dma_next < s_hi; ++dma_next) {
+    jt_dma = step_key0(dma_next);
+    issue_step(dma_next, jt_dma);
+  }
 
   // per-lane LDS byte offsets (as in attn_fwd_kernel)
   const int k_lane = lq * RP + 16 * k_slot<D>(lq, lh);
@@ -278,8 +291,6 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
     const int base = pass == 0 ? 0 : n0;
     const int it_lo = imax32(s_lo - base, 0), it_hi = imin32(s_hi - base, nt);
     if (it_lo >= it_hi) continue;
-    const TileRange tr = pass == 0 ? tr0 : tr1;
-
     const int row0 = blk * BM + 32 * wave;
     const bool valid = row0 < g.S;
     const int i = row0 + lq;  // this lane's query row
@@ -302,13 +313,27 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
     // this wavefront's tile classes: hull [ulo, uhi], common interval [ilo, ihi]
     const int ra = row0, rb = imin32(row0 + 31, g.S - 1);
     const int c_ulo = key_lo(g, ra), c_uhi = key_hi(g, rb), c_ilo = key_lo(g, rb), c_ihi = key_hi(g, ra);
-    auto key_class = [&](int c, int d) {  // keys [c, d] against this wavefront's rows
-      if (!valid) return (int)TILE_EMPTY;
-      const bool tail = d > g.S - 1;
-      if (!tail && d < g.prefix) return (int)TILE_FULL;
-      if (c_ulo > c_uhi || c > c_uhi || d < c_ulo) return c < g.prefix ? (int)TILE_PARTIAL : (int)TILE_EMPTY;
-      if (!tail && c >= c_ilo && d <= c_ihi) return (int)TILE_FULL;
-      return (int)TILE_PARTIAL;
+    // The class of the 32 keys [c, c + 31] against this wavefront's rows, as
+    // unsigned range checks on c (bounds set once per block):
+    //   FULL:    inside the prefix, or inside [c_ilo, c_ihi], and not past S - 1;
+    //   PARTIAL: otherwise, when some key lies in the prefix or [c_ulo, c_uhi];
+    //   EMPTY:   otherwise, and always for a wavefront without rows.
+    // An empty range is an origin of 2^30 (every c - origin then reads as an
+    // unsigned number far above the span).
+    constexpr int kNone = 1 << 30;
+    const int pfx = valid ? g.prefix : 0;
+    const int pf_hi = imin32(pfx, g.S) - 32;  // c <= pf_hi: the keys lie in the prefix and before S
+    const int bf_hi = imin32(c_ihi - 31, g.S - 32);
+    const bool has_bf = valid && bf_hi >= c_ilo;
+    const int bf_lo = has_bf ? c_ilo : kNone;
+    const uint32_t bf_span = has_bf ? (uint32_t)(bf_hi - c_ilo) : 0u;
+    const bool has_v = valid && c_ulo <= c_uhi;
+    const int v_lo = has_v ? c_ulo - 31 : kNone;
+    const uint32_t v_span = has_v ? (uint32_t)(c_uhi - (c_ulo - 31)) : 0u;
+    auto key_class = [&](int c) {
+      if (c <= pf_hi || (uint32_t)(c - bf_lo) <= bf_span) return (int)TILE_FULL;
+      if (c < pfx || (uint32_t)(c - v_lo) <= v_span) return (int)TILE_PARTIAL;
+      return (int)TILE_EMPTY;
     };
 
     f32x16_t oacc[DB];
@@ -329,16 +354,19 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
       }
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (dma_next < s_hi) issue_step(dma_next++);
-      const char* St = lds + (step % NS) * STAGE_BYTES;
-      const int jt0 = (pass == 0 && rot0 != 0) ? (a0 + it - rot0 + (it < rot0 ? n0 : 0)) * BN
-                                               : tile_at(tr, kRev ? nt - 1 - it : it) * BN;
+      const int jt0 = jt_dma;  // this step's first key
+      if (dma_next < s_hi) {
+        jt_dma = step_key0(dma_next);
+        issue_step(dma_next, jt_dma);
+        ++dma_next;
+      }
+      const char* St = lds + ((uint32_t)step & (NS - 1)) * STAGE_BYTES;
 
 #pragma unroll
       for (int kbs = 0; kbs < 2; ++kbs) {
         const int kb = kRev ? 1 - kbs : kbs;
         const int jb = jt0 + 32 * kb;
-        const int cls = key_class(jb, jb + 31);
+        const int cls = key_class(jb);
         if (cls == TILE_EMPTY) continue;
         const char* Kb = St + 32 * kb * RP;
         f32x16_t s;
