@@ -196,6 +196,43 @@ __device__ __forceinline__ void dma_rows(const uint16_t* base, int64_t rs, int r
   }
 }
 
+// dma_rows with its per-lane offsets computed once for a fixed row stride: a
+// tile whose 64 rows lie inside the sub-sequence adds only its uniform row
+// base, a 32 x 32 -> 64-bit product (rows are non-negative and a row step is
+// below 2^25 elements, so its byte count fits 32 bits); the last tile, whose
+// rows past the end are clamped, takes dma_rows.
+template <int D, int NW>
+struct RowDma {
+  static constexpr int DQ = D / 8, NDMA = 64 * DQ / (NW * 64);
+  uint32_t off[NDMA];
+  uint32_t row_bytes;
+  __device__ RowDma(int64_t rs, int wave, int lane) : row_bytes(2u * (uint32_t)rs) {
+#pragma unroll
+    for (int n = 0; n < NDMA; ++n) {
+      const int pos = (n * NW + wave) * 64 + lane;
+      const int r = pos / DQ, slot = pos % DQ;
+      off[n] = (uint32_t)r * row_bytes + 16 * k_slot<D>(r, slot);
+    }
+  }
+  __device__ void operator()(const uint16_t* base, int64_t rs, int row, int S, char* dst, int wave, int lane) const {
+    if (row + 64 <= S) {
+      const uint16_t* src = (const uint16_t*)((const char*)base + (uint64_t)(uint32_t)row * row_bytes);
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) dma16s(src, off[n], lds_addr(dst + (n * NW + wave) * 1024));
+    } else {
+      dma_rows<D, NW>(base, rs, row, S, dst, wave, lane);
+    }
+  }
+};
+
+// The stage of tile it + NS - 1 (the DMA's, one iteration ahead of the
+// compute's stage `cur` = it mod NS): without a division when NS is not a
+// power of two.
+template <int NS>
+__device__ __forceinline__ uint32_t stage_behind(uint32_t cur) {
+  return cur == 0 ? NS - 1 : cur - 1;
+}
+
 // Kernel set of one (head_dim, normaliser, ALiBi, softcap) instantiation.
 using BwdKernelFn = void (*)(BwdParams);
 struct BwdKernels {
@@ -315,15 +352,27 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
   const int t_lane = t_row * RP + 16 * k_slot<D>(t_row, 2 * (g16 & 1) + ((s16 & 3) >> 1)) + 8 * (s16 & 1);
   const int t_lane8 = (t_lane ^ (16 * row_swz<D>(8))) + 8 * RP;  // the same lanes 8 rows down
 
-  auto issue = [&](int it) {
-    const int jt0 = tile_at(tr, it) * BN;
-    char* st = lds + (it % NS) * STAGE_BYTES;
-    dma_rows<D, NW>(kh, krs, jt0, g.S, st, wave, lane);
-    dma_rows<D, NW>(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
+  // Scalar work per tile is kept small: a tile's first key is the previous
+  // tile's plus BN except at the seam between prefix and band tiles (and the
+  // first), separately for the DMA (NS - 1 tiles ahead) and the compute; the
+  // stage is a wrapping counter; the class comes from per-wavefront bounds
+  // (mask.h); the DMA's per-lane offsets are fixed once.
+  const int seam = tr.n_pre;
+  const RowDma<D, NW> kdma(krs, wave, lane), vdma(vrs, wave, lane);
+  auto issue = [&](int jt0, uint32_t stage) {
+    char* st = lds + stage * STAGE_BYTES;
+    kdma(kh, krs, jt0, g.S, st, wave, lane);
+    vdma(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
   };
   constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64));  // loads per tile per wavefront
-  int dma_next = 0;
-  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+  int dma_next = 0, jt_dma = 0;
+  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) {
+    jt_dma = (dma_next == 0 || dma_next == seam) ? tile_at(tr, dma_next) * BN : jt_dma + BN;
+    issue(jt_dma, (uint32_t)dma_next);
+  }
+  const KeyRanges<BN> kr(g, wvalid, ra, rb);
+  int jt0 = 0;
+  uint32_t st_cur = 0;
   // Q, dO and the row statistics in registers before the loop: otherwise the
   // compiler's waits for these loads sink into the loop, where their vmcnt
   // also drains the K/V tiles in flight (the compiler does not count the DMA)
@@ -349,10 +398,16 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dq_kernel(const
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (dma_next < ntiles) issue(dma_next++);
-    const char* St = lds + (it % NS) * STAGE_BYTES;
-    const int jt0 = tile_at(tr, it) * BN;
-    const int cls = wvalid ? classify_tile(g, ra, rb, jt0, jt0 + BN - 1) : (int)TILE_EMPTY;
+    const uint32_t st_it = st_cur;  // it mod NS
+    st_cur = st_it + 1 == NS ? 0 : st_it + 1;
+    if (dma_next < ntiles) {
+      jt_dma = dma_next == seam ? tile_at(tr, dma_next) * BN : jt_dma + BN;
+      issue(jt_dma, stage_behind<NS>(st_it));
+      ++dma_next;
+    }
+    const char* St = lds + st_it * STAGE_BYTES;
+    jt0 = (it == 0 || it == seam) ? tile_at(tr, it) * BN : jt0 + BN;
+    const int cls = key_class(kr, jt0);
     if (cls == TILE_EMPTY) continue;
 
     uint32_t pk[KB][8];  // dS^T, bf16 pairs
@@ -545,11 +600,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     }
   };
   Cursor dc = cursor0(), cc = cursor0();
-  auto issue = [&](int it) {
+  // Scalar work per tile is kept small: the stage is a wrapping counter, the
+  // class of a row tile comes from the wavefront's two row spans (mask.h), and
+  // the DMA's per-lane offsets are fixed once.
+  const RowDma<D, NW> qdma(qrs, wave, lane), dodma(dors, wave, lane);
+  const RowRanges<BM> rr(g, wvalid, kc, kd);
+  uint32_t st_cur = 0;
+  auto issue = [&](uint32_t stage) {
     const int i0 = dc.qt * BM;
-    char* st = lds + (it % NS) * STAGE_BYTES;
-    dma_rows<D, NW>(dc.qb, qrs, i0, g.S, st, wave, lane);
-    dma_rows<D, NW>(dc.dob, dors, i0, g.S, st + T_BYTES, wave, lane);
+    char* st = lds + stage * STAGE_BYTES;
+    qdma(dc.qb, qrs, i0, g.S, st, wave, lane);
+    dodma(dc.dob, dors, i0, g.S, st + T_BYTES, wave, lane);
     if constexpr (kStats) {
       // wavefront w moves 32 floats: lse log2 e rows [32 w, +32) (w < 2), or
       // -delta rows [32 (w - 2), +32); the stats rows are padded to 64
@@ -560,7 +621,7 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
   };
   constexpr int NDMA2 = 2 * (64 * (D / 8) / (NW * 64)) + (kStats ? 1 : 0);
   int dma_next = 0;
-  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue((uint32_t)dma_next);
   // K and V in registers before the loop (see the dQ kernel)
 #pragma unroll
   for (int kk = 0; kk < DK; ++kk) asm volatile("" : "+v"(kf[kk]), "+v"(vf[kk]));
@@ -571,12 +632,17 @@ __global__ __launch_bounds__(256, D == 64 ? 2 : 1) void attn_bwd_dkdv_kernel(con
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (dma_next < ntiles) issue(dma_next++);
-    const char* St = lds + (it % NS) * STAGE_BYTES;
+    const uint32_t st_it = st_cur;  // it mod NS
+    st_cur = st_it + 1 == NS ? 0 : st_it + 1;
+    if (dma_next < ntiles) {
+      issue(stage_behind<NS>(st_it));
+      ++dma_next;
+    }
+    const char* St = lds + st_it * STAGE_BYTES;
     const int hq = cc.hq, i0 = cc.qt * BM;
     advance(cc);
     // rows past the end of the sub-sequence are clamped copies: mask them
-    int cls = wvalid ? classify_tile(g, i0, imin32(i0 + BM - 1, g.S - 1), kc, kd) : (int)TILE_EMPTY;
+    int cls = row_class(rr, i0);
     if (cls == TILE_EMPTY) continue;
     if (i0 + BM > g.S) cls = TILE_PARTIAL;
     constexpr bool kSeed = ALIBI && !SOFTCAP;  // as in the dQ kernel

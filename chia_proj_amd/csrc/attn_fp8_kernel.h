@@ -213,14 +213,54 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
   const int t_src = q16 >> 1, p_src = q16 & 1, hh = grp >> 1;
   const int v_key = 4 * hh + (t_src & 3) + 8 * (t_src >> 2);  // + 16 wp
 
-  auto issue = [&](int it) {
-    const int jt0 = tile_at(tr, kRev ? ntiles - 1 - it : it) * BN;
-    char* st = lds + (it % NS) * STAGE_BYTES;
-    fp8_dma_rows<D>(kh, krs, jt0, g.S, st, wave, lane);
-    fp8_dma_rows<D>(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
+  // Scalar work per tile is kept small (it issues on the critical path with
+  // four wavefronts per SIMD): the stage by a mask where NS is a power of two;
+  // a tile's first key stepped by one tile from the previous one's, computed in
+  // full only at a block's first tile and at the seam between its prefix and
+  // band tiles (separately for the DMA, which runs NS - 1 tiles ahead, and the
+  // compute); the K / V row base a 32 x 32 -> 64-bit product (keys are
+  // non-negative, a row step is below 2^25 bytes); and on tiles inside the
+  // sub-sequence the DMA's per-lane offsets fixed once.
+  auto stage_of = [](int it) -> uint32_t {
+    if constexpr ((NS & (NS - 1)) == 0) return (uint32_t)it & (NS - 1);
+    else return (uint32_t)it % NS;
   };
-  int dma_next = 0;
-  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) issue(dma_next);
+  const int dkey = kRev ? -BN : BN;
+  const int seam = kRev ? tr.n2 : tr.n_pre;
+  auto tile_key = [&](int it) { return tile_at(tr, kRev ? ntiles - 1 - it : it) * BN; };
+  const uint32_t krs_u = (uint32_t)krs, vrs_u = (uint32_t)vrs;
+  constexpr int NDMA = BN * (D / 16) / 256;  // 1 KB loads per wavefront per tile (each of K, V)
+  uint32_t k_off[NDMA], v_off[NDMA];
+#pragma unroll
+  for (int n = 0; n < NDMA; ++n) {
+    const int pos = (n * 4 + wave) * 64 + lane;
+    const int row = pos / (D / 16), slot = pos % (D / 16);
+    k_off[n] = (uint32_t)row * krs_u + 16 * fp8_slot<D>(row, slot);
+    v_off[n] = (uint32_t)row * vrs_u + 16 * fp8_slot<D>(row, slot);
+  }
+  auto issue = [&](int it, int jt0) {
+    char* st = lds + stage_of(it) * STAGE_BYTES;
+    if (jt0 + BN <= g.S) {
+      const uint8_t* kt = kh + (uint64_t)(uint32_t)jt0 * krs_u;
+      const uint8_t* vt = vh + (uint64_t)(uint32_t)jt0 * vrs_u;
+#pragma unroll
+      for (int n = 0; n < NDMA; ++n) {
+        dma16s(kt, k_off[n], lds_addr(st + (n * 4 + wave) * 1024));
+        dma16s(vt, v_off[n], lds_addr(st + T_BYTES + (n * 4 + wave) * 1024));
+      }
+    } else {
+      fp8_dma_rows<D>(kh, krs, jt0, g.S, st, wave, lane);
+      fp8_dma_rows<D>(vh, vrs, jt0, g.S, st + T_BYTES, wave, lane);
+    }
+  };
+  int dma_next = 0, jt_dma = 0;
+  for (; dma_next < NS - 1 && dma_next < ntiles; ++dma_next) {
+    jt_dma = (dma_next == 0 || dma_next == seam) ? tile_key(dma_next) : jt_dma + dkey;
+    issue(dma_next, jt_dma);
+  }
+  // the class of a tile against this wavefront's rows (mask.h)
+  const KeyRanges<BN> kr(g, wvalid, ra, rb);
+  int jt0 = 0;
   // Q in registers before the loop: otherwise the compiler's wait for these
   // loads sinks into the loop as vmcnt(0), which also drains the K/V tiles in
   // flight on every tile (the compiler does not count the DMA)
@@ -237,10 +277,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_fp8_kernel(const Fp8Params p)
     }
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (dma_next < ntiles) issue(dma_next++);
-    const char* St = lds + (it % NS) * STAGE_BYTES;
-    const int jt0 = tile_at(tr, kRev ? ntiles - 1 - it : it) * BN;
-    const int cls = wvalid ? classify_tile(g, ra, rb, jt0, jt0 + BN - 1) : (int)TILE_EMPTY;
+    if (dma_next < ntiles) {
+      jt_dma = (dma_next == seam) ? tile_key(dma_next) : jt_dma + dkey;
+      issue(dma_next, jt_dma);
+      ++dma_next;
+    }
+    const char* St = lds + stage_of(it) * STAGE_BYTES;
+    jt0 = (it == 0 || it == seam) ? tile_key(it) : jt0 + dkey;
+    const int cls = key_class(kr, jt0);
     if (cls == TILE_EMPTY) continue;
 
     // S^T for the tile's two 32-key blocks

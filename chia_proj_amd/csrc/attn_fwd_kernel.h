@@ -87,6 +87,53 @@ constexpr float kRescaleLog2 = 8.0f;  // lazy-rescale threshold (log2 units)
 constexpr float kLazyBound = 65536.0f;  // partial row sum of one tile that triggers an exact max
 constexpr int kBN = 64;
 
+// KeyRanges<N>::classify (mask.h) as scalar compares and selects, for a key
+// offset the wavefront shares: ten scalar instructions, no branch.  The
+// compiler's form of the same tests combines 64-bit condition masks, about
+// twice the instructions, in a loop where scalar issue is on the critical path.
+template <int N>
+__device__ __forceinline__ int key_class(const KeyRanges<N>& kr, int c) {
+  static_assert(TILE_EMPTY == 0 && TILE_FULL == 1 && TILE_PARTIAL == 2, "class codes");
+  int cls, t;
+  asm("s_sub_u32 %1, %2, %5\n\t"
+      "s_cmp_le_u32 %1, %6\n\t"
+      "s_cselect_b32 %0, 2, 0\n\t"   // some key in the hull: PARTIAL
+      "s_cmp_lt_i32 %2, %7\n\t"
+      "s_cselect_b32 %0, 2, %0\n\t"  // the first key in the prefix: PARTIAL
+      "s_sub_u32 %1, %2, %3\n\t"
+      "s_cmp_le_u32 %1, %4\n\t"
+      "s_cselect_b32 %0, 1, %0\n\t"  // every key in the common interval: FULL
+      "s_cmp_le_i32 %2, %8\n\t"
+      "s_cselect_b32 %0, 1, %0"      // every key in the prefix: FULL
+      : "=&s"(cls), "=&s"(t)
+      : "s"(c), "s"(kr.bf_lo), "s"(kr.bf_span), "s"(kr.v_lo), "s"(kr.v_span), "s"(kr.pfx), "s"(kr.pf_hi)
+      : "scc");
+  return cls;
+}
+
+// RowRanges<M>::classify (mask.h) the same way, for a row tile start the
+// wavefront shares: twelve scalar instructions, no branch.
+template <int M>
+__device__ __forceinline__ int row_class(const RowRanges<M>& rr, int a) {
+  int cls, b, t, u;
+  asm("s_add_i32 %1, %4, %9\n\t"   // b = min(a + M - 1, S - 1)
+      "s_min_i32 %1, %1, %5\n\t"
+      "s_sub_i32 %2, %1, %6\n\t"
+      "s_sub_i32 %3, %7, %4\n\t"
+      "s_min_i32 %2, %2, %3\n\t"
+      "s_cmp_ge_i32 %2, 0\n\t"
+      "s_cselect_b32 %0, 2, 0\n\t"   // b >= v_lo and a <= v_hi: PARTIAL
+      "s_sub_i32 %2, %4, %8\n\t"
+      "s_sub_i32 %3, %10, %1\n\t"
+      "s_min_i32 %2, %2, %3\n\t"
+      "s_cmp_ge_i32 %2, 0\n\t"
+      "s_cselect_b32 %0, 1, %0"      // a >= f_lo and b <= f_hi: FULL
+      : "=&s"(cls), "=&s"(b), "=&s"(t), "=&s"(u)
+      : "s"(a), "s"(rr.last), "s"(rr.v_lo), "s"(rr.v_hi), "s"(rr.f_lo), "n"(M - 1), "s"(rr.f_hi)
+      : "scc");
+  return cls;
+}
+
 struct FwdParams {
   const uint16_t* q;
   const uint16_t* k;

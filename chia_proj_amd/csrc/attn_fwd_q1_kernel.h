@@ -231,14 +231,15 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
     k_dma[n] = (uint32_t)(2 * ((int64_t)row * krs + 8 * k_slot<D>(row, slot)));
     v_dma[n] = (uint32_t)(2 * ((int64_t)row * vrs + 8 * v_slot<D>(row, slot)));
   }
-  // The tile's row base in 32-bit unsigned arithmetic: keys and the K / V
-  // row strides (times the dilation) are non-negative and below 2^25.
+  // The tile's row base as a 32 x 32 -> 64-bit product: keys are
+  // non-negative, and a K / V row step (stride times dilation) is below 2^25
+  // elements, so its byte count fits 32 bits.
   static_assert((NS & (NS - 1)) == 0, "the stage index is a mask");
-  const uint32_t krs_u = (uint32_t)krs, vrs_u = (uint32_t)vrs;
+  const uint32_t k_row_bytes = 2u * (uint32_t)krs, v_row_bytes = 2u * (uint32_t)vrs;
   auto issue_step = [&](int s, int jt0) {
     char* kst = lds + ((uint32_t)s & (NS - 1)) * STAGE_BYTES;
-    const uint16_t* kt = kh + (uint64_t)(uint32_t)jt0 * krs_u;
-    const uint16_t* vt = vh + (uint64_t)(uint32_t)jt0 * vrs_u;
+    const uint16_t* kt = (const uint16_t*)((const char*)kh + (uint64_t)(uint32_t)jt0 * k_row_bytes);
+    const uint16_t* vt = (const uint16_t*)((const char*)vh + (uint64_t)(uint32_t)jt0 * v_row_bytes);
     if (jt0 + BN <= g.S) {
 #pragma unroll
       for (int n = 0; n < NDMA; ++n) {
@@ -262,10 +263,24 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
   // two stages one step is in flight: its first key, found for the DMA, is
   // the compute's key one iteration later (jt_dma).
   static_assert(NS == 2, "one step in flight");
+  // The DMA's keys are stepped: within a block a step's first key is the
+  // previous step's plus BN (minus BN walking backwards), except at the
+  // block's start, at the seam between its prefix and band tiles, and at the
+  // rotation's wrap, where step_key0 gives it in full.
+  const int dkey = kRev ? -BN : BN;
+  const int seam0 = rot0 != 0 ? rot0 : (kRev ? tr0.n2 : tr0.n_pre);
+  const int seam1 = n0 + (kRev ? tr1.n2 : tr1.n_pre);
+  auto next_break = [&](int s) {  // the first step after s whose key is not stepped
+    if (s < seam0) return seam0;
+    if (s < n0) return n0;
+    if (s < seam1) return seam1;
+    return 0x7fffffff;
+  };
   int dma_next = s_lo;
-  int jt_dma = 0;
+  int jt_dma = 0, brk = 0;
   for (; dma_next < s_lo + NS - 1 && dma_next < s_hi; ++dma_next) {
     jt_dma = step_key0(dma_next);
+    brk = next_break(dma_next);
     issue_step(dma_next, jt_dma);
   }
 
@@ -310,31 +325,8 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
         qf[kk] = __builtin_bit_cast(bf16x8_t, val);
       }
     }
-    // this wavefront's tile classes: hull [ulo, uhi], common interval [ilo, ihi]
-    const int ra = row0, rb = imin32(row0 + 31, g.S - 1);
-    const int c_ulo = key_lo(g, ra), c_uhi = key_hi(g, rb), c_ilo = key_lo(g, rb), c_ihi = key_hi(g, ra);
-    // The class of the 32 keys [c, c + 31] against this wavefront's rows, as
-    // unsigned range checks on c (bounds set once per block):
-    //   FULL:    inside the prefix, or inside [c_ilo, c_ihi], and not past S - 1;
-    //   PARTIAL: otherwise, when some key lies in the prefix or [c_ulo, c_uhi];
-    //   EMPTY:   otherwise, and always for a wavefront without rows.
-    // An empty range is an origin of 2^30 (every c - origin then reads as an
-    // unsigned number far above the span).
-    constexpr int kNone = 1 << 30;
-    const int pfx = valid ? g.prefix : 0;
-    const int pf_hi = imin32(pfx, g.S) - 32;  // c <= pf_hi: the keys lie in the prefix and before S
-    const int bf_hi = imin32(c_ihi - 31, g.S - 32);
-    const bool has_bf = valid && bf_hi >= c_ilo;
-    const int bf_lo = has_bf ? c_ilo : kNone;
-    const uint32_t bf_span = has_bf ? (uint32_t)(bf_hi - c_ilo) : 0u;
-    const bool has_v = valid && c_ulo <= c_uhi;
-    const int v_lo = has_v ? c_ulo - 31 : kNone;
-    const uint32_t v_span = has_v ? (uint32_t)(c_uhi - (c_ulo - 31)) : 0u;
-    auto key_class = [&](int c) {
-      if (c <= pf_hi || (uint32_t)(c - bf_lo) <= bf_span) return (int)TILE_FULL;
-      if (c < pfx || (uint32_t)(c - v_lo) <= v_span) return (int)TILE_PARTIAL;
-      return (int)TILE_EMPTY;
-    };
+    // the class of a 32-key step against this wavefront's rows (mask.h)
+    const KeyRanges<32> kr(g, valid, row0, imin32(row0 + 31, g.S - 1));
 
     f32x16_t oacc[DB];
 #pragma unroll
@@ -356,7 +348,12 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
       asm volatile("" ::: "memory");
       const int jt0 = jt_dma;  // this step's first key
       if (dma_next < s_hi) {
-        jt_dma = step_key0(dma_next);
+        if (dma_next == brk) {
+          jt_dma = step_key0(dma_next);
+          brk = next_break(dma_next);
+        } else {
+          jt_dma += dkey;
+        }
         issue_step(dma_next, jt_dma);
         ++dma_next;
       }
@@ -366,7 +363,7 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
       for (int kbs = 0; kbs < 2; ++kbs) {
         const int kb = kRev ? 1 - kbs : kbs;
         const int jb = jt0 + 32 * kb;
-        const int cls = key_class(jb);
+        const int cls = key_class(kr, jb);
         if (cls == TILE_EMPTY) continue;
         const char* Kb = St + 32 * kb * RP;
         f32x16_t s;

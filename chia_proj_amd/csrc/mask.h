@@ -132,6 +132,38 @@ CHIA_HD int32_t classify_tile(const MaskGeom& g, int32_t a, int32_t b, int32_t c
   return TILE_PARTIAL;
 }
 
+// classify_tile(g, a, b, c, c + N - 1) for one block of rows [a, b] and any
+// key offset c, as range checks on c from bounds set once per block:
+// FULL when the keys lie in the prefix, or in the rows' common interval
+// [key_lo(b), key_hi(a)], and not past S - 1; otherwise PARTIAL when some key
+// lies in the prefix or in the hull [key_lo(a), key_hi(b)]; otherwise EMPTY,
+// and always when the block has no rows (valid false).  An empty range has
+// the origin 2^30: c - origin then reads as an unsigned number above any span
+// (and an empty prefix bound is -2^30, below any key).
+template <int N>
+struct KeyRanges {
+  int32_t pfx, pf_hi, bf_lo, v_lo;
+  uint32_t bf_span, v_span;
+  CHIA_HD KeyRanges(const MaskGeom& g, bool valid, int32_t a, int32_t b) {
+    constexpr int32_t kNone = 1 << 30;
+    const int32_t ulo = key_lo(g, a), uhi = key_hi(g, b), ilo = key_lo(g, b), ihi = key_hi(g, a);
+    pfx = valid ? g.prefix : -kNone;                        // c < pfx: the first key lies in the prefix
+    pf_hi = valid ? imin32(g.prefix, g.S) - N : -kNone;     // c <= pf_hi: all N keys do, before S
+    const int32_t bf_hi = imin32(ihi - (N - 1), g.S - N);
+    const bool has_bf = valid && bf_hi >= ilo;
+    bf_lo = has_bf ? ilo : kNone;
+    bf_span = has_bf ? (uint32_t)(bf_hi - ilo) : 0u;
+    const bool has_v = valid && ulo <= uhi;
+    v_lo = has_v ? ulo - (N - 1) : kNone;
+    v_span = has_v ? (uint32_t)(uhi - v_lo) : 0u;
+  }
+  CHIA_HD int32_t classify(int32_t c) const {
+    if (c <= pf_hi || (uint32_t)(c - bf_lo) <= bf_span) return TILE_FULL;
+    if (c < pfx || (uint32_t)(c - v_lo) <= v_span) return TILE_PARTIAL;
+    return TILE_EMPTY;
+  }
+};
+
 // Band key tiles (index t, keys [bn t, bn t + bn - 1], t >= the prefix tiles)
 // whose classes for two query blocks [a0, b0], [a1, b1] (v0 / v1: the block
 // has rows) are known without classify_tile: [pf_lo, pf_hi] where both blocks
@@ -217,6 +249,37 @@ CHIA_HD RowSpan query_range(const MaskGeom& g, int32_t j0, int32_t j1) {
   }
   return RowSpan{first, lo - 1};
 }
+
+// classify_tile(g, a, min(a + M - 1, S - 1), c, d) for fixed keys [c, d]
+// (c <= S - 1) and any row tile start a (0 <= a <= S - 1), from two row
+// spans found once: the rows that see some key of [c, d] (query_range(c, d):
+// key_hi(i) >= c and key_lo(i) <= d, or every row when c is in the prefix)
+// and those that see all of them (query_range(d, c): key_hi(i) >= d and
+// key_lo(i) <= c, or every row when d is in the prefix; none when d runs past
+// S - 1).  FULL when the tile lies inside the second span, PARTIAL when it
+// meets the first, EMPTY otherwise and for keys without a wavefront
+// (valid false).  Exact because key_lo and key_hi are non-decreasing and
+// every row sees its own key (key_lo(i) <= i <= key_hi(i)).
+template <int M>
+struct RowRanges {
+  int32_t f_lo, f_hi, v_lo, v_hi, last;
+  CHIA_HD RowRanges(const MaskGeom& g, bool valid, int32_t c, int32_t d) {
+    constexpr int32_t kNone = 1 << 30;  // an empty span: no tile reaches it
+    last = g.S - 1;
+    const RowSpan v = valid ? query_range(g, c, d) : RowSpan{kNone, -kNone};
+    const RowSpan f = valid && d <= g.S - 1 ? query_range(g, d, c) : RowSpan{kNone, -kNone};
+    v_lo = v.lo;
+    v_hi = v.hi;
+    f_lo = f.lo;
+    f_hi = f.hi;
+  }
+  CHIA_HD int32_t classify(int32_t a) const {
+    const int32_t b = imin32(a + M - 1, last);
+    if (a >= f_lo && b <= f_hi) return TILE_FULL;
+    if (b >= v_lo && a <= v_hi) return TILE_PARTIAL;
+    return TILE_EMPTY;
+  }
+};
 
 // KV tiles of width bn that queries [a, b] may touch: [0, n_pre) followed by
 // [start2, start2 + n2).

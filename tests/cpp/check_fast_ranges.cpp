@@ -2,7 +2,9 @@
 // against classify_tile: every band key tile the kernel runs without
 // classification must have the class the fast path assumes, in every
 // wavefront for the workgroup-uniform WIDE span; and of hidden_bits (the
-// per-element mask of partial blocks) against visible().  Built and run by
+// per-element mask of partial blocks) against visible(); and of KeyRanges
+// and RowRanges (the per-step classes from per-block bounds) against
+// classify_tile.  Built and run by
 // tests/test_mask_fast_ranges.py; exits non-zero on the first mismatch.
 #include <cstdio>
 #include <initializer_list>
@@ -86,11 +88,79 @@ static int check_query_range(long* n) {
   return 0;
 }
 
+// KeyRanges<N>::classify (the kernels' per-step class from bounds set once
+// per row block) against classify_tile for every 32-row block of a wavefront,
+// and every key offset c (multiples of 4, past both ends), N = 32 and 64;
+// a block without rows is EMPTY everywhere.
+template <int N>
+static int check_key_ranges_n(const MaskGeom& g, long* n, const char* tag) {
+  for (int a = 0; a < g.S + 64; a += 32) {
+    const bool valid = a < g.S;
+    const int b = imin32(a + 31, g.S - 1);
+    const KeyRanges<N> kr(g, valid, a, b);
+    for (int c = -2 * N; c < g.S + 2 * N; c += 4) {
+      const int want = valid ? classify_tile(g, a, b, c, c + N - 1) : (int)TILE_EMPTY;
+      ++*n;
+      if (kr.classify(c) != want) {
+        std::printf("KeyRanges<%d> mismatch %s a=%d c=%d got %d want %d\n", N, tag, a, c, kr.classify(c), want);
+        return 1;
+      }
+    }
+  }
+  return 0;
+}
+
+// RowRanges<M>::classify (the dK/dV kernel's per-tile class of its query row
+// tiles against a wavefront's fixed 32 keys) against classify_tile, for every
+// 32-aligned key block and every row tile start of either tile height.
+template <int M>
+static int check_row_ranges_m(const MaskGeom& g, long* n, const char* tag) {
+  for (int c = 0; c < g.S; c += 32) {
+    const int d = c + 31;
+    for (int valid = 0; valid < 2; ++valid) {
+      const RowRanges<M> rr(g, valid != 0, c, d);
+      for (int a = 0; a < g.S; a += (M > 32 ? 16 : 8)) {
+        const int want = valid ? classify_tile(g, a, imin32(a + M - 1, g.S - 1), c, d) : (int)TILE_EMPTY;
+        ++*n;
+        if (rr.classify(a) != want) {
+          std::printf("RowRanges<%d> mismatch %s c=%d a=%d valid=%d got %d want %d\n", M, tag, c, a, valid,
+                      rr.classify(a), want);
+          return 1;
+        }
+      }
+    }
+  }
+  return 0;
+}
+
+static int check_key_ranges(long* n) {
+  for (int S : {1, 31, 64, 97, 200, 513, 1024})
+    for (int causal = 0; causal < 2; ++causal)
+      for (int w : {0, 1, 5, 64, 129, 300})
+        for (int d : {1, 2, 3})
+          for (int blk : {0, 33, 128})
+            for (int pre : {0, 40, 130, 2000}) {
+              if (d > 1 && pre > 0) continue;
+              const MaskSpec m = make_mask_spec(S, causal, w, d, blk, pre);
+              char tag[96];
+              std::snprintf(tag, sizeof tag, "S=%d c=%d w=%d d=%d blk=%d p=%d", S, causal, w, d, blk, pre);
+              for (int r = 0; r < num_residues(m); ++r) {
+                const MaskGeom g = residue_geom(m, r);
+                if (g.S <= 0) continue;
+                if (check_key_ranges_n<32>(g, n, tag) || check_key_ranges_n<64>(g, n, tag)) return 1;
+                if (check_row_ranges_m<64>(g, n, tag) || check_row_ranges_m<128>(g, n, tag)) return 1;
+              }
+            }
+  return 0;
+}
+
 int main() {
   const int bn = 64;
   long n_bits = 0, n_rows = 0;
   if (check_hidden_bits(&n_bits)) return 1;
   if (check_query_range(&n_rows)) return 1;
+  long n_class = 0;
+  if (check_key_ranges(&n_class)) return 1;
   long checked = 0, fast = 0, wide_all = 0;
   const int seqs[] = {1, 63, 64, 65, 200, 511, 700, 1024};
   const int windows[] = {0, 1, 5, 64, 129, 300};
@@ -172,7 +242,8 @@ int main() {
                 }
               }
             }
-  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span, %ld mask bits, %ld query-range rows\n",
-              checked, fast, wide_all, n_bits, n_rows);
+  std::printf("checked %ld band tiles, %ld on a fast path, %ld in a workgroup WIDE span, %ld mask bits, %ld query-range rows, "
+              "%ld key-range classes\n",
+              checked, fast, wide_all, n_bits, n_rows, n_class);
   return 0;
 }

@@ -1,5 +1,6 @@
 """CPU checks of chia_proj_amd/csrc/mask.h by brute force: the kernel's
-unclassified fast paths (fast_ranges, wide_range_all) against classify_tile over
+unclassified fast paths (fast_ranges, wide_range_all) and per-block class bounds
+(KeyRanges) against classify_tile over
 masks, residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp), and
 the multiply-high divider against plain division (tests/cpp/check_udiv.cpp),
 the LDS tile layout against a bank model (tests/cpp/check_lds_banks.cpp) and
@@ -22,7 +23,7 @@ def test_fast_ranges_agree_with_classification(tmp_path):
                     str(ROOT / "tests" / "cpp" / "check_fast_ranges.cpp"), "-o", str(exe)], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
-    assert "on a fast path" in out.stdout
+    assert "on a fast path" in out.stdout and "key-range classes" in out.stdout
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
