@@ -22,6 +22,12 @@ import torch
 GATE_MAX_ABS = 2e-2
 GATE_MEAN_ABS = 2e-3
 REL_TOL = 3e-2
+# Scale-aware tolerances (unnormalised sigmoid / ReLU outputs), relative to
+# M = max|ref|: about twice the largest ratio the GPU suite's 563 scale-aware
+# checks measure (max-abs 5.3e-3 M, mean-abs 5.3e-4 M), never below the
+# absolute gate.  Rounding an output to bf16 alone moves it by up to 2^-8 M.
+SCALED_MAX_ABS = 1e-2
+SCALED_MEAN_ABS = 1e-3
 SCALES = (("standard", 1.0), ("small", 0.01))
 
 
@@ -64,13 +70,15 @@ def _finite_status(ref: torch.Tensor, out) -> str:
 
 
 def north_star_gate(ref: torch.Tensor, out: torch.Tensor, max_abs: float = GATE_MAX_ABS,
-                    mean_abs: float = GATE_MEAN_ABS, scale_aware: bool = False) -> GateResult:
+                    mean_abs: float = GATE_MEAN_ABS, scale_aware: bool = False,
+                    scaled_max_abs: float = SCALED_MAX_ABS, scaled_mean_abs: float = SCALED_MEAN_ABS) -> GateResult:
     """bf16 `out` against fp32 `ref`: max-abs <= 2e-2 and mean-abs <= 2e-3.
 
-    scale_aware=True multiplies both tolerances by max(1, max|ref|).  It is for
-    the unnormalised sigmoid / ReLU outputs at the reference's default
-    parameters (no 1/S or -log S), whose magnitude grows like sqrt(S): rounding
-    an output of magnitude 32 to bf16 alone moves it by up to 0.0625.
+    scale_aware=True allows max(max_abs, scaled_max_abs M) and
+    max(mean_abs, scaled_mean_abs M), M = max|ref|.  It is for the unnormalised
+    sigmoid / ReLU outputs at the reference's default parameters (no 1/S or
+    -log S), whose magnitude grows like sqrt(S): rounding an output of
+    magnitude 32 to bf16 alone moves it by up to 0.0625.
     """
     st = _finite_status(ref, out)
     if st:
@@ -78,7 +86,10 @@ def north_star_gate(ref: torch.Tensor, out: torch.Tensor, max_abs: float = GATE_
     stats = error_stats(ref, out)
     mag = max(1.0, ref.detach().float().abs().max().item()) if scale_aware else 1.0
     stats["tol_scale"] = mag
-    ok = stats["max_abs"] <= max_abs * mag and stats["mean_abs"] <= mean_abs * mag
+    tol_max = max(max_abs, scaled_max_abs * mag) if scale_aware else max_abs
+    tol_mean = max(mean_abs, scaled_mean_abs * mag) if scale_aware else mean_abs
+    stats["tol_max_abs"], stats["tol_mean_abs"] = tol_max, tol_mean
+    ok = stats["max_abs"] <= tol_max and stats["mean_abs"] <= tol_mean
     return GateResult(ok, "OK" if ok else "incorrect", stats)
 
 

@@ -59,7 +59,14 @@ def test_north_star_gate_thresholds():
     assert not gate.north_star_gate(big, o).ok
     o2 = big.clone()
     o2[0, 0] += 0.1
-    assert gate.north_star_gate(big, o2, scale_aware=True).ok  # 0.1 <= 2e-2 * 30
+    assert gate.north_star_gate(big, o2, scale_aware=True).ok  # 0.1 <= 1e-2 * 30
+    o2[0, 0] = 30.0 + 0.31
+    assert not gate.north_star_gate(big, o2, scale_aware=True).ok  # 0.31 > 1e-2 * 30
+    # never tighter than the absolute gate: M = 1.5 keeps max-abs 2e-2
+    small = torch.full((4, 64), 1.5)
+    o3 = small.clone()
+    o3[0, 0] += 0.019
+    assert gate.north_star_gate(small, o3, scale_aware=True).ok
     assert gate.north_star_gate(r, r[:, :3]).status == "wrong shape"
     assert gate.north_star_gate(r, r * float("nan")).status == "NaN"
 
