@@ -3,8 +3,9 @@ unclassified fast paths (fast_ranges, wide_range_all) and per-block class bounds
 (KeyRanges) against classify_tile over
 masks, residues, row blocks and key tiles (tests/cpp/check_fast_ranges.cpp), and
 the multiply-high divider against plain division (tests/cpp/check_udiv.cpp),
-the LDS tile layout against a bank model (tests/cpp/check_lds_banks.cpp) and
-the paired core's DMA / barrier schedule (tests/cpp/check_schedule.cpp), all
+the LDS tile layout against a bank model (tests/cpp/check_lds_banks.cpp),
+the paired core's DMA / barrier schedule (tests/cpp/check_schedule.cpp) and the
+one-block core's stepped tile keys (tests/cpp/check_tile_keys.cpp), all
 built with AddressSanitizer and UndefinedBehaviorSanitizer."""
 import shutil
 import subprocess
@@ -80,3 +81,19 @@ def test_one_block_split_schedule_is_safe(tmp_path):
     planted = subprocess.run([str(exe), "planted"], capture_output=True, text=True)
     assert planted.returncode == 0, planted.stdout + planted.stderr
     assert planted.stdout.count("planted mistake") == 4
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="g++ not available")
+def test_stepped_tile_keys(tmp_path):
+    """The one-block core's stepped tile keys (the full key only at a block's start, the
+    prefix/band seam and the rotation's wrap) against the full formula, over random tile
+    ranges, walk directions and group starts; each of two planted break mistakes is caught."""
+    exe = tmp_path / "check_tile_keys"
+    subprocess.run(["g++", "-std=c++17", "-O1", *SANITIZE, f"-I{ROOT / 'chia_proj_amd' / 'csrc'}",
+                    str(ROOT / "tests" / "cpp" / "check_tile_keys.cpp"), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "0 stepped keys differ" in out.stdout
+    planted = subprocess.run([str(exe), "planted"], capture_output=True, text=True)
+    assert planted.returncode == 0, planted.stdout + planted.stderr
+    assert planted.stdout.count("planted mistake") == 2
