@@ -18,7 +18,7 @@
 //     modifier, where sharing each K/V tile between two row blocks halves the
 //     K/V reads.
 //   * head_dim 64, banded masks: a workgroup's key range is its rows plus the
-//     window, a few tiles; four wavefronts per SIMD (~110 VGPRs) hide the
+//     window, a few tiles; four wavefronts per SIMD (103-126 VGPRs) hide the
 //     latency of those few tiles better than the paired core's two.  Causal
 //     rows (a prefix, or softmax on large grids): one block per workgroup,
 //     launched longest-first, balances them where zigzag pairs measured slower.
