@@ -19,10 +19,10 @@ namespace chia {
 
 using KernelFn = void (*)(FwdParams);
 KernelFn select_kernel_d64(int waves, int norm, bool alibi, bool softcap);
-KernelFn select_q1_kernel_d64(int norm, bool alibi, bool softcap);
+KernelFn select_q1_kernel_d64(int norm, bool alibi, bool softcap, bool cap_fixed);
 KernelFn select_kernel_d128(int norm);
-KernelFn select_q1_kernel_d128(int norm, bool alibi, bool softcap);
-KernelFn select_q1_split_kernel_d128(int norm, bool alibi, bool softcap);
+KernelFn select_q1_kernel_d128(int norm, bool alibi, bool softcap, bool cap_fixed);
+KernelFn select_q1_split_kernel_d128(int norm, bool alibi, bool softcap, bool cap_fixed);
 BwdKernels select_bwd_kernels_d64(int norm, bool alibi, bool softcap);
 BwdKernels select_bwd_kernels_d128(int norm, bool alibi, bool softcap);
 Fp8KernelFn select_fp8_kernel(int head_dim, int format, int norm, bool alibi, bool softcap);
@@ -287,10 +287,15 @@ int launch_fwd(const chia_attn_args* a, float* lse, void* stream) {
   p.post_scale = a->post_scale;
   p.lse = a->norm == CHIA_ATTN_NORM_SOFTMAX ? lse : nullptr;
 
-  KernelFn fn = a->head_dim == 64 ? (geo.q1 ? select_q1_kernel_d64((int)a->norm, sp.alibi, sp.softcap)
+  // Softcap softmax on the one-block core: weights against a fixed reference
+  // when cap log2 e <= 78 (cap <= 54), which keeps every weight normal
+  // (attn_fwd_q1_kernel.h); north star 208.7 -> 200.6 us, headline 66.7 ->
+  // 62.7 us against the running max.
+  const bool cap_fixed = sp.softcap && a->norm == CHIA_ATTN_NORM_SOFTMAX && a->softcap * kLog2e <= 78.0f;
+  KernelFn fn = a->head_dim == 64 ? (geo.q1 ? select_q1_kernel_d64((int)a->norm, sp.alibi, sp.softcap, cap_fixed)
                                             : select_kernel_d64(waves, (int)a->norm, sp.alibi, sp.softcap))
-               : geo.q1            ? (geo.groups == 2 ? select_q1_split_kernel_d128((int)a->norm, sp.alibi, sp.softcap)
-                                                  : select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap))
+               : geo.q1            ? (geo.groups == 2 ? select_q1_split_kernel_d128((int)a->norm, sp.alibi, sp.softcap, cap_fixed)
+                                                  : select_q1_kernel_d128((int)a->norm, sp.alibi, sp.softcap, cap_fixed))
                                    : select_kernel_d128((int)a->norm);
   if (fn == nullptr) return CHIA_ATTN_ERR_NORM;  // no instantiation for this core and normaliser
   void* kargs[] = {&p};

@@ -55,10 +55,13 @@ struct Q1Config {
 };
 
 // NG = 2: the workgroup holds two groups of four wavefronts that split one
-// zigzag pair's steps between them (below); NG = 1: one group.
-template <int D, int NORM, bool ALIBI, bool SOFTCAP, int NG = 1>
+// zigzag pair's steps between them (below); NG = 1: one group.  CAPFIX
+// (softcap softmax with cap log2 e <= 78, chosen by the host): the weights are
+// taken against a fixed reference (below) instead of a running max.
+template <int D, int NORM, bool ALIBI, bool SOFTCAP, int NG = 1, bool CAPFIX = false>
 __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_kernel(const FwdParams p) {
   static_assert(NG == 1 || NG == 2, "one or two groups");
+  static_assert(!CAPFIX || (SOFTCAP && NORM == NORM_SOFTMAX), "the fixed reference is for softcap softmax");
   constexpr int NW = 4;  // wavefronts per group
   constexpr int BN = kBN;
   constexpr int NT = NW * 64;
@@ -295,6 +298,12 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
   // wavefront runs its exponentials beside them (sigmoid and ReLU measured
   // slower with either)
   constexpr bool kPrio = NORM == NORM_SOFTMAX;
+  // Softcap softmax with cap log2 e <= 78 (cap <= 54; the host checks): a
+  // score is below cap log2 e = sc_b, so the fixed reference m = sc_b - 48
+  // keeps every weight in (2^(48 - 2 sc_b), 2^48], normal in fp32 and bf16:
+  // no max, no vote on the row sum, no rescale.  (With a larger cap a row whose
+  // scores all lie near -cap would fall below the normal range.)
+  const float m_fix = sc_b - 48.0f;
   int step = s_lo;
   bool merged = false;
 #pragma unroll 1
@@ -333,7 +342,7 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[db][e] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+    float m_run = CAPFIX ? m_fix : -INFINITY, l_run = 0.f;
 
 #pragma unroll 1
     for (int it = it_lo; it < it_hi; ++it, ++step) {
@@ -468,7 +477,10 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
           };
           float lt = 0.f;
           bool exact = true;
-          if constexpr (kLazy) {
+          if constexpr (CAPFIX) {
+            exps(m_run, 0.f, lt);  // m_run is the fixed reference
+            exact = false;
+          } else if constexpr (kLazy) {
             exact = __any(m_run == -INFINITY);
             if (!exact) {
               exps(m_run, 0.f, lt);
@@ -501,7 +513,7 @@ __global__ __launch_bounds__(256 * NG, Q1Config<D>::occupancy) void attn_fwd_q1_
             const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
             exps(m_use, kLazy ? 0.f : l_run, lt);
           }
-          l_run = kLazy ? l_run + lt : lt;
+          l_run = (kLazy || CAPFIX) ? l_run + lt : lt;
         } else {
 #pragma unroll
           for (int w = 0; w < 8; ++w) {

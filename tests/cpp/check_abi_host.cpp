@@ -32,10 +32,10 @@ struct BwdKernels {
   BwdKernelFn stats, dq, dkdv;
 };
 KernelFn select_kernel_d64(int, int, bool, bool) { return nullptr; }
-KernelFn select_q1_kernel_d64(int, bool, bool) { return nullptr; }
+KernelFn select_q1_kernel_d64(int, bool, bool, bool) { return nullptr; }
 KernelFn select_kernel_d128(int) { return nullptr; }
-KernelFn select_q1_kernel_d128(int, bool, bool) { return nullptr; }
-KernelFn select_q1_split_kernel_d128(int, bool, bool) { return nullptr; }
+KernelFn select_q1_kernel_d128(int, bool, bool, bool) { return nullptr; }
+KernelFn select_q1_split_kernel_d128(int, bool, bool, bool) { return nullptr; }
 BwdKernels select_bwd_kernels_d64(int, bool, bool) { return BwdKernels{nullptr, nullptr, nullptr}; }
 BwdKernels select_bwd_kernels_d128(int, bool, bool) { return BwdKernels{nullptr, nullptr, nullptr}; }
 Fp8KernelFn select_fp8_kernel(int, int, int, bool, bool) { return nullptr; }

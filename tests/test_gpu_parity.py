@@ -168,6 +168,7 @@ RISING = [
     ("block256", dict(causal=False, block=256)),
     ("window200_softcap30", dict(causal=True, window=200, softcap=30.0)),
     ("local100_dil2", dict(causal=False, window=100, dilation=2)),
+    ("softcap80", dict(causal=True, softcap=80.0)),  # above the fixed-reference limit: the running max
 ]
 
 
@@ -273,6 +274,35 @@ def test_softmax_rising_scores(name, kw, shape, D):
 def test_softmax_rising_scores_paired_causal(name, kw):
     """The same on causal rows of the paired core's 4-wavefront workgroups (B2 H16 S4096 D64)."""
     _rising_case(name, kw, PAIRED_CAUSAL, 64)
+
+
+@pytest.mark.parametrize("cap", [30.0, 54.0])
+@pytest.mark.parametrize("shape,D,kw", [((4, 16, 1024), 64, dict(causal=True)), ((1, 2, 512), 64, dict(causal=True, window=300)),
+                                        ((1, 2, 512), 128, dict(causal=True))],
+                         ids=["B4H16S1024_d64_causal", "B1H2S512_d64_window", "B1H2S512_d128_causal"])
+def test_softcap_fixed_reference_saturated(cap, shape, D, kw):
+    """Softcap softmax with a cap up to 54 takes its weights against the fixed reference
+    cap log2 e - 48 on the one-block core (these shapes run it).  Keys of the first half are
+    -50 u and queries 50 u (u a unit vector), so those scores sit at -cap: rows of the first
+    half see only weights at the bottom of the range, 2^(48 - 2 cap log2 e), which must stay
+    normal; keys of the second half are +50 u, scores at +cap, weights at the top, 2^48."""
+    B, H, S = shape
+    _say(f"[parity] softcap fixed reference cap={cap} {shape} D{D} {kw}")
+    g = torch.Generator("cpu").manual_seed(int(cap) + S + D)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    sign = torch.where(torch.arange(S) < S // 2, -1.0, 1.0)
+    k = (50.0 * sign[:, None] * u + 0.1 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
+    q = (50.0 * u + 0.1 * torch.randn(B, H, S, D, generator=g)).to(torch.bfloat16)
+    v = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    o = attention(q.to(DEV), k.to(DEV), v.to(DEV), softcap=cap, **kw)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o).all())
+    oc = o.float().cpu()
+    for b, h in [(0, 0), (B - 1, H - 1)]:
+        r = oracle.attention_ref(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], softcap=cap, **kw)
+        res = gate.north_star_gate(r[0, 0], oc[b, h])
+        assert res.ok, f"cap={cap} b={b} h={h}: {res.status} {res.stats}"
 
 
 def test_strided_layout_and_out_param():
